@@ -1,0 +1,218 @@
+/*
+ * oxide_sampler.h — C ABI of the MI355X (gfx950) batched token sampler.
+ *
+ * This is the drop-in boundary for the hot path of the reference engine's CPU
+ * sampler, crates/oxide-core/src/sampler.rs (AcademicSamplerEngine::sample_token,
+ * sampler.rs:173-390). One call samples a whole batch of rows on the GPU, on the
+ * caller's HIP stream, with the reference's chain and per-row configuration:
+ *
+ *   mask -> bans -> biases -> newline penalty -> repetition / frequency /
+ *   presence penalties -> temperature -> top-M (M = max(top_k, 256)) -> softmax
+ *   -> Mirostat v1/v2 | (min-p -> XTC -> top-k -> tail-free -> locally typical
+ *   -> top-p -> renormalise -> inverse-CDF draw)
+ *
+ * Conventions (mirroring the reference's FFI precedent,
+ * crates/oxide-hardware/oxide-backend-cuda/src/driver.rs:671-690):
+ *   - int return, 0 = success, negative = error (OXS_ERR_*);
+ *   - device pointers are plain typed pointers (DevicePtr<T>,
+ *     crates/oxide-core/src/memory.rs:9), never dereferenced on the host;
+ *   - the stream argument is last and is a hipStream_t passed as void*;
+ *   - all device workspace is allocated once by oxs_sampler_create (the
+ *     preallocated-arena pattern of crates/oxide-alloc/src/device_arena.rs:7-80),
+ *     so oxs_sample_batch allocates nothing, never synchronises and makes no
+ *     host round trip.
+ *
+ * Ties between equal logits are broken by the lower token index.
+ */
+#ifndef OXIDE_SAMPLER_H
+#define OXIDE_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OXS_ABI_VERSION 1u
+
+/* Return codes. EngineError (crates/oxide-core/src/error.rs:6) has one variant
+ * on this path, ShapeMismatch (error.rs:52; sampler.rs:179-181). */
+#define OXS_OK 0
+#define OXS_ERR_INVALID_ARGUMENT (-1)
+#define OXS_ERR_SHAPE_MISMATCH (-2) /* vocab == 0, as sampler.rs:179-181 */
+#define OXS_ERR_LIMITS (-3)         /* batch/vocab/top_k beyond oxs_limits */
+#define OXS_ERR_HIP (-4)            /* a HIP runtime call failed */
+#define OXS_ERR_UNSUPPORTED (-5)    /* a feature this build does not run on the GPU */
+#define OXS_ERR_NO_DEVICE (-6)
+
+/* Per-row outcome written to out_status[b]. */
+#define OXS_ROW_OK 0            /* Ok(token); token recorded (sampler.rs:387) */
+#define OXS_ROW_EMPTY 1         /* every logit -inf or NaN: Ok(0), nothing recorded (sampler.rs:267-270) */
+#define OXS_ROW_HISTORY_FULL 2  /* Ok(token), but the device history had no room to record it */
+#define OXS_ROW_UNSUPPORTED 3   /* the row asks for a stage this build does not run on the GPU; token 0 */
+#define OXS_ROW_MISSING_STATE 4 /* a Mirostat row but oxs_batch.mirostat_mu is NULL; token 0 */
+
+/* MirostatMode, sampler.rs:77-82. */
+#define OXS_MIROSTAT_DISABLED 0
+#define OXS_MIROSTAT_V1 1
+#define OXS_MIROSTAT_V2 2
+
+/* Logits element type. The reference is f32 only (sampler.rs:175); bf16 rows
+ * are widened exactly (bits << 16) before the chain. */
+#define OXS_DTYPE_F32 0
+#define OXS_DTYPE_BF16 1
+
+/* oxs_batch.flags */
+#define OXS_FLAG_RECORD_HISTORY 1u  /* append the sampled token(s) to history (record_token, sampler.rs:155-157) */
+#define OXS_FLAG_SHARED_CONFIG 2u   /* configs points at ONE config used by every row */
+
+/*
+ * SamplingConfig (sampler.rs:17-42) for one row, as plain scalars. The Rust
+ * usize fields are narrowed to uint32. logit_biases (a HashMap<u32,f32>) and
+ * banned_tokens (a HashSet<u32>) become ranges into the batch's CSR arrays
+ * (oxs_batch.bias_ids/bias_values and oxs_batch.ban_ids). A bias list that
+ * repeats an id behaves like repeated HashMap::insert: the last entry wins.
+ * newline_token_id is sample_token's third argument (sampler.rs:177).
+ * The seed field of SamplingConfig maps to the row's rng_state
+ * (see oxs_rng_state_from_seed).
+ */
+typedef struct oxs_sampling_config {
+  float temperature;
+  uint32_t top_k;
+  float top_p;
+  float min_p;
+  float tfs_z;
+  float typical_p;
+  float xtc_threshold;
+  float xtc_probability;
+  int32_t mirostat_mode;
+  float mirostat_tau;
+  float mirostat_eta;
+  float dry_multiplier;
+  float dry_base;
+  uint32_t dry_allowed_length;
+  uint32_t dry_range;
+  float repeat_penalty;
+  uint32_t repeat_last_n;
+  float frequency_penalty;
+  float presence_penalty;
+  uint32_t penalize_nl;
+  float newline_penalty;
+  uint32_t newline_token_id;
+  uint32_t bias_offset;
+  uint32_t bias_count;
+  uint32_t ban_offset;
+  uint32_t ban_count;
+} oxs_sampling_config;
+
+/* Sizes fixed at create time; every workspace buffer is sized from these. */
+typedef struct oxs_limits {
+  uint32_t max_batch;  /* rows per call */
+  uint32_t max_vocab;  /* V per row */
+  uint32_t max_top_k;  /* largest top_k any row may use; 0 means 256 */
+} oxs_limits;
+
+/*
+ * One batched sampling call. Every pointer is a device pointer unless noted.
+ * Row b's state (the reference's SamplerState, sampler.rs:86-91) is:
+ *   history[b*history_ld .. + history_len[b]]  generated_tokens
+ *   mirostat_mu[b]                              mirostat_mu
+ *   rng_state[b]                                rng_state (xorshift64, sampler.rs:139-153)
+ * and its candidates_buffer after the call is out_kept_ids/out_kept_probs.
+ */
+typedef struct oxs_batch {
+  uint32_t batch;         /* rows B */
+  uint32_t vocab;         /* V */
+  int32_t logits_dtype;   /* OXS_DTYPE_* */
+  uint32_t flags;         /* OXS_FLAG_* */
+  int64_t logits_ld;      /* elements between consecutive rows (>= vocab) */
+  const void* logits;     /* [B][logits_ld], read only */
+
+  const oxs_sampling_config* configs; /* [B], or [1] with OXS_FLAG_SHARED_CONFIG */
+  const uint32_t* bias_ids;           /* CSR arrays indexed by the config ranges (may be NULL if unused) */
+  const float* bias_values;
+  const uint32_t* ban_ids;
+
+  const uint32_t* allowed_mask; /* optional [B][mask_ld] words: bit (i%32) of word i/32 set = token i allowed */
+  int64_t mask_ld;
+
+  uint32_t* history;      /* [B][history_ld] token ids (may be NULL when every history_len is 0 and nothing is recorded) */
+  int64_t history_ld;
+  uint32_t* history_len;  /* [B]; updated when OXS_FLAG_RECORD_HISTORY is set */
+  uint32_t history_cap;   /* room per row for recording (<= history_ld) */
+
+  const float* uniforms;  /* optional [B] u in [0,1): replaces state.next_f32() (sampler.rs:374) */
+  uint64_t* rng_state;    /* optional [B]; advanced by one draw when uniforms is NULL */
+  float* mirostat_mu;     /* [B] in/out; required when any row uses Mirostat */
+
+  uint32_t* out_tokens;   /* [B] sampled token ids */
+  int32_t* out_status;    /* optional [B] OXS_ROW_* */
+  uint32_t* out_kept_count; /* optional [B] size of candidates_buffer after the call */
+  uint32_t* out_kept_ids;   /* optional [B][kept_ld] */
+  float* out_kept_probs;    /* optional [B][kept_ld] */
+  int64_t kept_ld;
+
+  /* Optional [B][logits_out_ld] f32: receives each row's logits after bans,
+   * biases, newline and window penalties and temperature, i.e. what the
+   * reference leaves in its `logits: &mut [f32]` argument (sampler.rs:184-254;
+   * checked by academic_samplers_test.rs:75), with masked ids at -inf. Must not
+   * overlap `logits`. */
+  float* logits_out;
+  int64_t logits_out_ld;
+} oxs_batch;
+
+typedef struct oxs_sampler oxs_sampler;
+
+/* ABI version of the loaded library (OXS_ABI_VERSION at build time). */
+uint32_t oxs_abi_version(void);
+
+/* Human-readable text for an OXS_* return code. */
+const char* oxs_status_string(int code);
+
+/* SamplingConfig::default() (sampler.rs:44-73), with newline_token_id = 0 and
+ * empty bias/ban ranges. */
+void oxs_sampling_config_default(oxs_sampling_config* cfg);
+
+/* Initial rng_state of SamplerState::new (has_seed = 0) or
+ * SamplerState::new_with_seed (sampler.rs:104-128; seed 0 maps to the default). */
+uint64_t oxs_rng_state_from_seed(int has_seed, uint64_t seed);
+
+/* Initial mirostat_mu of SamplerState::new(tau) = 2 * tau (sampler.rs:108). */
+float oxs_mirostat_mu_from_tau(float tau);
+
+/*
+ * Creates a sampler on HIP device `device`, allocating every device buffer it
+ * will ever need. Replaces AcademicSamplerEngine::new (sampler.rs:168), which
+ * owned no device state. Not thread-safe; one sampler per stream.
+ */
+int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device);
+
+/* Frees the sampler's device workspace. Waits for nothing: the caller must
+ * have synchronised the streams it used. */
+int oxs_sampler_destroy(oxs_sampler* sampler);
+
+/* Bytes of device workspace the sampler holds. */
+size_t oxs_sampler_workspace_bytes(const oxs_sampler* sampler);
+
+/*
+ * Samples every row of `batch` on `stream` (a hipStream_t; NULL = default
+ * stream). Replaces B serial calls of
+ *   AcademicSamplerEngine::sample_token(&self, logits: &mut [f32],
+ *       state: &mut SamplerState, newline_token_id: u32) -> Result<u32>
+ * (sampler.rs:173-178) at continuous_batching.rs:970-973 and
+ * oxide-backend-cuda/src/lib.rs:3302/:6057. Asynchronous and stream ordered:
+ * results are valid once the stream reaches this point. `logits` is read
+ * only; the reference's in-place side effect is available through
+ * oxs_batch.logits_out.
+ * Returns OXS_ERR_SHAPE_MISMATCH for vocab == 0, OXS_ERR_LIMITS when the batch
+ * exceeds the create-time limits, OXS_ERR_INVALID_ARGUMENT for missing
+ * required pointers, OXS_ERR_HIP if the launch fails.
+ */
+int oxs_sample_batch(oxs_sampler* sampler, const oxs_batch* batch, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* OXIDE_SAMPLER_H */

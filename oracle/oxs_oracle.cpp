@@ -1,0 +1,431 @@
+// oxs_oracle.cpp — CPU restatement of crates/oxide-core/src/sampler.rs.
+//
+// TEST INFRASTRUCTURE ONLY (see oxs_oracle.h): the checker for the GPU
+// sampler and the CPU baseline of bench.py. Build: oracle/Makefile
+// (g++ -O2 -ffp-contract=off, no fast-math, glibc libm).
+#include "oxs_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <thread>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+namespace {
+
+struct Cand {
+  uint32_t id;
+  float p;
+};
+
+// Descending by value, ties by lower token index. Candidates never hold NaN
+// (they are filtered by `l > -inf`, sampler.rs:263), and -0.0 == +0.0 here as
+// under f32::partial_cmp (sampler.rs:277, :283).
+inline bool cand_desc(const Cand& a, const Cand& b) {
+  if (a.p > b.p) return true;
+  if (a.p < b.p) return false;
+  return a.id < b.id;
+}
+
+// Rust's f32 Iterator::sum folds from -0.0 (sampler.rs:360, :494-497).
+inline float rust_sum_init() { return -0.0f; }
+
+// sampler.rs:393-415: DRY. For match_len from 32 down to allowed_len, every
+// earlier occurrence of the history suffix of that length penalises the token
+// that followed it; penalties accumulate in loop order.
+void apply_dry_penalty(const oxs_sampling_config& c, float* logits, uint32_t vocab,
+                       const uint32_t* history, uint32_t history_len) {
+  uint32_t scan_start = history_len > c.dry_range ? history_len - c.dry_range : 0;
+  const uint32_t* h = history + scan_start;
+  uint32_t n = history_len - scan_start;
+  if (c.dry_allowed_length > 32) return;  // (allowed..=32).rev() is empty
+  for (int64_t match_len = 32; match_len >= (int64_t)c.dry_allowed_length; --match_len) {
+    if ((int64_t)n < match_len) continue;
+    const uint32_t* suffix = h + (n - match_len);
+    int64_t upto = (int64_t)n - match_len;  // saturating_sub: n >= match_len here
+    for (int64_t i = 0; i < upto; ++i) {
+      bool eq = true;
+      for (int64_t j = 0; j < match_len; ++j) {
+        if (h[i + j] != suffix[j]) { eq = false; break; }
+      }
+      if (!eq) continue;
+      uint32_t next_token = h[i + match_len];  // i + match_len < n always
+      float exponent = (float)(uint64_t)(match_len - c.dry_allowed_length);
+      float pw = powf(c.dry_base, exponent);
+      float penalty = c.dry_multiplier * pw;
+      if (next_token < vocab) logits[next_token] -= penalty;
+    }
+  }
+}
+
+// sampler.rs:459-490: tail-free sampling on the (un-renormalised) sorted list.
+void apply_tail_free_sampling(const oxs_sampling_config& c, std::vector<Cand>& cand) {
+  size_t n = cand.size();
+  if (n < 3) return;
+  std::vector<float> d1(n - 1), d2(n - 2);
+  for (size_t i = 0; i + 1 < n; ++i) d1[i] = cand[i].p - cand[i + 1].p;
+  float sum_d2 = 0.0f;
+  for (size_t i = 0; i + 1 < d1.size(); ++i) {
+    float diff = fabsf(d1[i] - d1[i + 1]);
+    d2[i] = diff;
+    sum_d2 += diff;
+  }
+  if (sum_d2 <= 0.0f) return;
+  float inv_sum = 1.0f / sum_d2;
+  float cum = 0.0f;
+  size_t cutoff = n;
+  for (size_t i = 0; i < d2.size(); ++i) {
+    float t = d2[i] * inv_sum;
+    cum += t;
+    if (cum >= c.tfs_z) { cutoff = i + 1; break; }
+  }
+  cand.resize(std::max<size_t>(cutoff, 1));
+}
+
+// sampler.rs:493-520: locally typical sampling. Re-orders the candidates by
+// |surprisal - entropy| (stable sort) and keeps the prefix reaching typical_p.
+void apply_locally_typical_sampling(const oxs_sampling_config& c, std::vector<Cand>& cand) {
+  float entropy = rust_sum_init();
+  for (const Cand& x : cand) {
+    float term = x.p > 0.0f ? (-x.p) * logf(x.p) : 0.0f;
+    entropy += term;
+  }
+  struct Scored { uint32_t id; float p; float diff; };
+  std::vector<Scored> scored(cand.size());
+  for (size_t i = 0; i < cand.size(); ++i) {
+    float surprisal = cand[i].p > 0.0f ? -logf(cand[i].p) : 0.0f;
+    scored[i] = {cand[i].id, cand[i].p, fabsf(surprisal - entropy)};
+  }
+  std::stable_sort(scored.begin(), scored.end(),
+                   [](const Scored& a, const Scored& b) { return a.diff < b.diff; });
+  float cum = 0.0f;
+  std::vector<Cand> keep;
+  for (const Scored& s : scored) {
+    cum += s.p;
+    keep.push_back({s.id, s.p});
+    if (cum >= c.typical_p) break;
+  }
+  cand.swap(keep);
+}
+
+struct RowIo {
+  uint32_t* history;
+  uint32_t* history_len;
+  uint32_t history_cap;
+  bool record;
+  float* mu;
+  uint64_t* rng_state;
+  const float* uniform;
+  uint32_t* token;
+  uint32_t* kept_ids;
+  float* kept_probs;
+  uint32_t* kept_count;
+  uint32_t kept_cap;
+};
+
+// Appends to generated_tokens (SamplerState::record_token, sampler.rs:155-157).
+bool record(RowIo& io, uint32_t tok) {
+  if (!io.record) return true;
+  if (*io.history_len >= io.history_cap) return false;
+  io.history[(*io.history_len)++] = tok;
+  return true;
+}
+
+void write_kept(RowIo& io, const std::vector<Cand>& cand) {
+  if (io.kept_count) *io.kept_count = (uint32_t)cand.size();
+  size_t n = std::min<size_t>(cand.size(), io.kept_cap);
+  for (size_t i = 0; i < n; ++i) {
+    if (io.kept_ids) io.kept_ids[i] = cand[i].id;
+    if (io.kept_probs) io.kept_probs[i] = cand[i].p;
+  }
+}
+
+// AcademicSamplerEngine::sample_token, sampler.rs:173-390.
+int sample_row(const oxs_sampling_config& c, const uint32_t* bias_ids, const float* bias_values,
+               const uint32_t* ban_ids, float* logits, uint32_t vocab, RowIo& io) {
+  const float NEG_INF = -INFINITY;
+  if (vocab == 0) return OXO_SHAPE_MISMATCH;  // :179-181
+
+  // 1. Bans, then biases (:184-193). A HashMap holds each id once; a repeated
+  // id in the CSR list behaves like repeated insert (last wins).
+  for (uint32_t k = 0; k < c.ban_count; ++k) {
+    uint32_t id = ban_ids[c.ban_offset + k];
+    if (id < vocab) logits[id] = NEG_INF;
+  }
+  for (uint32_t k = 0; k < c.bias_count; ++k) {
+    uint32_t id = bias_ids[c.bias_offset + k];
+    bool later = false;
+    for (uint32_t j = k + 1; j < c.bias_count; ++j)
+      if (bias_ids[c.bias_offset + j] == id) { later = true; break; }
+    if (later) continue;
+    if (id < vocab) logits[id] += bias_values[c.bias_offset + k];
+  }
+
+  // 2. Newline penalty (:196-200).
+  if (c.penalize_nl && c.newline_token_id < vocab) logits[c.newline_token_id] -= c.newline_penalty;
+
+  const uint32_t hist_len = *io.history_len;
+  // 3. DRY (:203-205).
+  if (c.dry_multiplier > 0.0f && hist_len > 0) apply_dry_penalty(c, logits, vocab, io.history, hist_len);
+
+  // 3b. Sliding-window repetition, frequency and presence penalties (:208-246).
+  if (hist_len > 0) {
+    uint32_t window_len = c.repeat_last_n > 0 ? c.repeat_last_n : hist_len;
+    uint32_t start = hist_len > window_len ? hist_len - window_len : 0;
+    const uint32_t* w = io.history + start;
+    uint32_t wn = hist_len - start;
+    if (fabsf(c.repeat_penalty - 1.0f) > 1e-5f && c.repeat_penalty > 0.0f) {
+      std::unordered_set<uint32_t> seen;
+      for (uint32_t j = 0; j < wn; ++j) {
+        uint32_t tok = w[j];
+        if (seen.insert(tok).second && tok < vocab) {
+          float& l = logits[tok];
+          if (l > 0.0f) l /= c.repeat_penalty;
+          else l *= c.repeat_penalty;
+        }
+      }
+    }
+    if (fabsf(c.frequency_penalty) > 1e-5f || fabsf(c.presence_penalty) > 1e-5f) {
+      std::unordered_map<uint32_t, uint64_t> counts;
+      for (uint32_t j = 0; j < wn; ++j) counts[w[j]] += 1;
+      for (const auto& kv : counts) {
+        if (kv.first < vocab) {
+          float t = (float)kv.second * c.frequency_penalty;
+          float pen = t + c.presence_penalty;
+          logits[kv.first] -= pen;
+        }
+      }
+    }
+  }
+
+  // 4. Temperature, skipped under Mirostat (:249-254).
+  if (c.temperature > 0.0f && c.mirostat_mode == OXS_MIROSTAT_DISABLED) {
+    float inv_temp = 1.0f / c.temperature;
+    for (uint32_t i = 0; i < vocab; ++i) logits[i] *= inv_temp;
+  }
+
+  // 5. Candidate pool: every id with l > -inf (drops -inf and NaN) (:257-265).
+  std::vector<Cand> cand;
+  cand.reserve(1024);
+  for (uint32_t i = 0; i < vocab; ++i)
+    if (logits[i] > NEG_INF) cand.push_back({i, logits[i]});
+  if (cand.empty()) {  // :267-270
+    *io.token = 0;
+    write_kept(io, cand);
+    return OXO_EMPTY;
+  }
+
+  // Keep the top max(top_k, 256) and sort them descending (:274-283).
+  size_t filter_k = std::min<size_t>(std::max<size_t>(c.top_k, 256), cand.size());
+  if (filter_k < cand.size()) {
+    std::nth_element(cand.begin(), cand.begin() + (filter_k - 1), cand.end(), cand_desc);
+    cand.resize(filter_k);
+  }
+  std::sort(cand.begin(), cand.end(), cand_desc);
+
+  // Softmax over the kept candidates only (:286-295).
+  float max_logit = cand[0].p;
+  float sum_exp = 0.0f;
+  for (Cand& x : cand) {
+    x.p = expf(x.p - max_logit);
+    sum_exp += x.p;
+  }
+  float inv_sum = sum_exp > 0.0f ? 1.0f / sum_exp : 1.0f;
+  for (Cand& x : cand) x.p *= inv_sum;
+
+  bool ok = true;
+  // 6. Mirostat (:298-312; v1 :418-429; v2 :432-456). The token is recorded
+  // twice: inside the mode function and again by the caller.
+  if (c.mirostat_mode == OXS_MIROSTAT_V1) {
+    uint32_t selected = cand[0].id;
+    float prob = fmaxf(cand[0].p, 1e-6f);
+    float surprise = -log2f(prob);
+    float error = surprise - c.mirostat_tau;
+    float step = c.mirostat_eta * error;
+    *io.mu -= step;
+    ok &= record(io, selected);
+    ok &= record(io, selected);
+    *io.token = selected;
+    write_kept(io, cand);
+    return ok ? OXO_OK : OXO_HISTORY_FULL;
+  }
+  if (c.mirostat_mode == OXS_MIROSTAT_V2) {
+    float max_surprise = *io.mu;
+    size_t cutoff = 1;
+    float cum_prob = 0.0f;
+    for (size_t i = 0; i < cand.size(); ++i) {
+      float surprise = -log2f(fmaxf(cand[i].p, 1e-8f));
+      if (surprise > max_surprise && i > 0) break;
+      cum_prob += cand[i].p;
+      cutoff = i + 1;
+    }
+    (void)cutoff;
+    uint32_t selected = cand[0].id;
+    float prob = cand[0].p / fmaxf(cum_prob, 1e-6f);
+    float surprise = -log2f(fmaxf(prob, 1e-8f));
+    float error = surprise - c.mirostat_tau;
+    float step = c.mirostat_eta * error;
+    *io.mu -= step;
+    ok &= record(io, selected);
+    ok &= record(io, selected);
+    *io.token = selected;
+    write_kept(io, cand);
+    return ok ? OXO_OK : OXO_HISTORY_FULL;
+  }
+
+  // 7. Min-p (:315-319): retain p >= p_max * min_p (a filter, not a prefix cut).
+  if (c.min_p > 0.0f && !cand.empty()) {
+    float threshold = cand[0].p * c.min_p;
+    std::vector<Cand> kept;
+    for (const Cand& x : cand)
+      if (x.p >= threshold) kept.push_back(x);
+    cand.swap(kept);
+  }
+  // 8. XTC (:322-328): deterministically drop the top choice.
+  if (c.xtc_probability > 0.0f && cand.size() > 1) {
+    float p_max = cand[0].p;
+    if (p_max >= c.xtc_threshold && p_max < 0.98f) cand.erase(cand.begin());
+  }
+  // 9. Top-k (:331-333).
+  if (c.top_k > 0 && cand.size() > c.top_k) cand.resize(c.top_k);
+  // 10. Tail-free (:336-338).
+  if (c.tfs_z < 1.0f && cand.size() > 2) apply_tail_free_sampling(c, cand);
+  // 11. Locally typical (:341-343).
+  if (c.typical_p < 1.0f && cand.size() > 1) apply_locally_typical_sampling(c, cand);
+  // 12. Top-p (:346-357).
+  if (c.top_p < 1.0f) {
+    float cumulative = 0.0f;
+    size_t cut = cand.size();
+    for (size_t i = 0; i < cand.size(); ++i) {
+      cumulative += cand[i].p;
+      if (cumulative >= c.top_p) { cut = std::min(i + 1, cand.size()); break; }
+    }
+    cand.resize(cut);
+  }
+  // Renormalise (:360-368).
+  float total = rust_sum_init();
+  for (const Cand& x : cand) total += x.p;
+  float inv_total = total > 0.0f ? 1.0f / total : 1.0f;
+  for (Cand& x : cand) x.p *= inv_total;
+
+  // Draw (:371-385): greedy below 1e-6, else the first candidate whose
+  // running sum reaches r; the fallback is the first candidate.
+  uint32_t picked;
+  if (c.temperature <= 1e-6f) {
+    picked = cand.empty() ? 0 : cand[0].id;
+  } else {
+    uint64_t fallback_state = 0x853c49e6748fea9bull;  // SamplerState::default() (:98)
+    float r = io.uniform ? *io.uniform : oxo_next_f32(io.rng_state ? io.rng_state : &fallback_state);
+    float acc = 0.0f;
+    uint32_t selected = cand.empty() ? 0 : cand[0].id;
+    for (const Cand& x : cand) {
+      acc += x.p;
+      if (r <= acc) { selected = x.id; break; }
+    }
+    picked = selected;
+  }
+  ok &= record(io, picked);  // :387
+  *io.token = picked;
+  write_kept(io, cand);
+  return ok ? OXO_OK : OXO_HISTORY_FULL;
+}
+
+inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t oxo_next_u64(uint64_t* state) {
+  uint64_t x = *state;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  *state = x;
+  return x;
+}
+
+float oxo_next_f32(uint64_t* state) {
+  uint32_t val = (uint32_t)(oxo_next_u64(state) >> 40);
+  return (float)val / 16777216.0f;
+}
+
+int oxo_sample_token(const oxs_sampling_config* cfg, const uint32_t* bias_ids,
+                     const float* bias_values, const uint32_t* ban_ids, float* logits,
+                     uint32_t vocab, uint32_t* history, uint32_t* history_len,
+                     uint32_t history_cap, float* mu, uint64_t* rng_state,
+                     const float* uniform, uint32_t* token, uint32_t* kept_ids,
+                     float* kept_probs, uint32_t* kept_count, uint32_t kept_cap) {
+  RowIo io{history, history_len, history_cap, true, mu, rng_state, uniform,
+           token, kept_ids, kept_probs, kept_count, kept_cap};
+  return sample_row(*cfg, bias_ids, bias_values, ban_ids, logits, vocab, io);
+}
+
+int oxo_sample_batch(const oxs_batch* b, int n_threads) {
+  if (b->vocab == 0) return OXO_SHAPE_MISMATCH;
+  auto work = [b](uint32_t lo, uint32_t hi) {
+    std::vector<float> row(b->vocab);
+    for (uint32_t r = lo; r < hi; ++r) {
+      const oxs_sampling_config& c = b->configs[(b->flags & OXS_FLAG_SHARED_CONFIG) ? 0 : r];
+      if (b->logits_dtype == OXS_DTYPE_BF16) {
+        const uint16_t* src = (const uint16_t*)b->logits + (size_t)r * b->logits_ld;
+        for (uint32_t i = 0; i < b->vocab; ++i) row[i] = bf16_to_f32(src[i]);
+      } else {
+        const float* src = (const float*)b->logits + (size_t)r * b->logits_ld;
+        memcpy(row.data(), src, sizeof(float) * b->vocab);
+      }
+      if (b->allowed_mask) {
+        const uint32_t* m = b->allowed_mask + (size_t)r * b->mask_ld;
+        for (uint32_t i = 0; i < b->vocab; ++i)
+          if (!((m[i >> 5] >> (i & 31)) & 1u)) row[i] = -INFINITY;
+      }
+      uint32_t zero_len = 0;
+      uint32_t* hist = b->history ? b->history + (size_t)r * b->history_ld : nullptr;
+      uint32_t* hlen = b->history_len ? &b->history_len[r] : &zero_len;
+      uint32_t local_len = *hlen;
+      bool rec = (b->flags & OXS_FLAG_RECORD_HISTORY) != 0;
+      float mu_dummy = 0.0f;
+      uint32_t tok = 0;
+      RowIo io{hist, rec ? hlen : &local_len, b->history_cap, rec,
+               b->mirostat_mu ? &b->mirostat_mu[r] : &mu_dummy,
+               b->rng_state ? &b->rng_state[r] : nullptr,
+               b->uniforms ? &b->uniforms[r] : nullptr, &tok,
+               b->out_kept_ids ? b->out_kept_ids + (size_t)r * b->kept_ld : nullptr,
+               b->out_kept_probs ? b->out_kept_probs + (size_t)r * b->kept_ld : nullptr,
+               b->out_kept_count ? &b->out_kept_count[r] : nullptr,
+               (uint32_t)b->kept_ld};
+      int st = sample_row(c, b->bias_ids, b->bias_values, b->ban_ids, row.data(), b->vocab, io);
+      if (b->logits_out) memcpy(b->logits_out + (size_t)r * b->logits_out_ld, row.data(), sizeof(float) * b->vocab);
+      b->out_tokens[r] = tok;
+      if (b->out_status) b->out_status[r] = st;
+    }
+  };
+  if (n_threads <= 1 || b->batch <= 1) {
+    work(0, b->batch);
+  } else {
+    uint32_t nt = std::min<uint32_t>((uint32_t)n_threads, b->batch);
+    std::vector<std::thread> ts;
+    for (uint32_t t = 0; t < nt; ++t) {
+      uint32_t lo = (uint32_t)((uint64_t)b->batch * t / nt);
+      uint32_t hi = (uint32_t)((uint64_t)b->batch * (t + 1) / nt);
+      ts.emplace_back(work, lo, hi);
+    }
+    for (auto& t : ts) t.join();
+  }
+  return 0;
+}
+
+float oxo_expf(float x) { return expf(x); }
+float oxo_logf(float x) { return logf(x); }
+float oxo_log2f(float x) { return log2f(x); }
+float oxo_powf(float x, float y) { return powf(x, y); }
+
+}  // extern "C"

@@ -1,0 +1,77 @@
+/*
+ * oxs_oracle.h — CPU restatement of the reference sampler, for tests only.
+ *
+ * TEST INFRASTRUCTURE. Nothing in the product links, loads or calls this
+ * code: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * use it, as the checker and the CPU baseline.
+ *
+ * It restates crates/oxide-core/src/sampler.rs stage by stage (each function
+ * cites the lines it follows) in C++ built with -O2 -ffp-contract=off and no
+ * fast-math, calling the platform libm's expf/logf/log2f/powf exactly where
+ * Rust's f32::{exp, ln, log2, powf} do, so on the same host it produces the
+ * same floats as the Rust code.
+ *
+ * Two deliberate differences from the reference, both part of the parity
+ * contract:
+ *   - the draw may use an injected uniform instead of state.next_f32();
+ *   - ties between equal logits are ordered by the lower token index (the
+ *     reference leaves the order after select_nth_unstable_by unspecified,
+ *     sampler.rs:276).
+ */
+#ifndef OXS_ORACLE_H
+#define OXS_ORACLE_H
+
+#include <stdint.h>
+#include "../include/oxide_sampler.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OXO_OK 0
+#define OXO_EMPTY 1            /* Ok(0) without record_token (sampler.rs:267-270) */
+#define OXO_HISTORY_FULL 2     /* sampled, but history_cap reached */
+#define OXO_SHAPE_MISMATCH (-2)
+
+/* SamplerState::next_u64 / next_f32 (sampler.rs:139-153). */
+uint64_t oxo_next_u64(uint64_t* state);
+float oxo_next_f32(uint64_t* state);
+
+/*
+ * AcademicSamplerEngine::sample_token (sampler.rs:173-390) on one row.
+ *   cfg, bias_ids/bias_values/ban_ids: the row's SamplingConfig (CSR ranges
+ *       of cfg index these arrays);
+ *   logits[vocab]: mutated in place exactly as the reference does;
+ *   history[*history_len] (capacity history_cap): generated_tokens, appended;
+ *   mu: mirostat_mu; rng_state: used only when uniform is NULL;
+ *   kept_ids/kept_probs (capacity kept_cap, may be NULL): candidates_buffer.
+ * Returns OXO_OK / OXO_EMPTY / OXO_HISTORY_FULL / OXO_SHAPE_MISMATCH and the
+ * token in *token (0 when empty).
+ */
+int oxo_sample_token(const oxs_sampling_config* cfg, const uint32_t* bias_ids,
+                     const float* bias_values, const uint32_t* ban_ids, float* logits,
+                     uint32_t vocab, uint32_t* history, uint32_t* history_len,
+                     uint32_t history_cap, float* mu, uint64_t* rng_state,
+                     const float* uniform, uint32_t* token, uint32_t* kept_ids,
+                     float* kept_probs, uint32_t* kept_count, uint32_t kept_cap);
+
+/*
+ * The same descriptor as oxs_sample_batch, with HOST pointers, sampled row by
+ * row (the packed mask is applied first by writing -inf, as the reference's
+ * grammar maskers do). Logits are copied per row, so the input is not
+ * modified. n_threads > 1 splits rows statically over that many threads.
+ * Returns 0 or OXO_SHAPE_MISMATCH.
+ */
+int oxo_sample_batch(const oxs_batch* batch, int n_threads);
+
+/* glibc's expf etc., exported so tests can compare the device emulation. */
+float oxo_expf(float x);
+float oxo_logf(float x);
+float oxo_log2f(float x);
+float oxo_powf(float x, float y);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

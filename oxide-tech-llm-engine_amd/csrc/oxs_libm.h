@@ -1,0 +1,206 @@
+// Single-precision exp/ln/log2 that reproduce, bit for bit, the glibc >= 2.27
+// implementations that Rust's f32::{exp, ln, log2} lower to on x86_64-linux-gnu.
+//
+// The reference sampler (crates/oxide-core/src/sampler.rs:289 exp, :424 and
+// :440/:451 log2, :496/:502 ln) calls the platform libm. glibc's single
+// precision routines are the published ARM optimized-routines algorithms
+// (Szabolcs Nagy, 2017; MIT licence): evaluate in double precision with a
+// 32-entry 2^(i/32) table (exp) or a 16-entry (1/c, log c) table (ln, log2) and
+// a short polynomial, then round once to float. Because every step is plain
+// IEEE double arithmetic, the same sequence of operations on the GPU's IEEE
+// f64 units yields the same float.
+//
+// glibc builds these routines twice on x86_64 and picks one at load time
+// (ifunc): a generic build and an FMA build in which the compiler fuses each
+// multiply feeding an add. The two builds differ in the last bit for a small
+// fraction of inputs, so both are provided here: OXS_LIBM_FMA selects the fused
+// form. The host library decides which one the host's libm uses (see
+// oxs_host_libm_variant in oxs_api.cpp) so the device matches the CPU the
+// reference sampler would run on.
+//
+// This header compiles as HIP device code and as plain host C++ (for the
+// tests that sweep it against the host libm). Build with -ffp-contract=off.
+#pragma once
+#include <stdint.h>
+#include <string.h>
+
+#if defined(__HIPCC__)
+#define OXS_HD __host__ __device__ __forceinline__
+#define OXS_CONST_TABLE __device__ __constant__
+#else
+#define OXS_HD static inline
+#define OXS_CONST_TABLE static const
+#include <math.h>
+#endif
+
+namespace oxs_libm {
+
+OXS_HD uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+OXS_HD float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+OXS_HD uint64_t d2u(double x) { uint64_t u; memcpy(&u, &x, 8); return u; }
+OXS_HD double u2d(uint64_t u) { double x; memcpy(&x, &u, 8); return x; }
+
+OXS_HD double fma_d(double a, double b, double c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_fma(a, b, c);
+#else
+  return fma(a, b, c);
+#endif
+}
+
+// a*b + c, either fused (one rounding) or as two rounded operations.
+template <bool FUSED>
+OXS_HD double mad(double a, double b, double c) {
+  if (FUSED) return fma_d(a, b, c);
+  double p = a * b;
+  return p + c;
+}
+
+// 2^(i/32) as double bits, minus i<<47 so that adding k<<47 scales by 2^(k/32).
+// Each entry is the correctly rounded double of 2^(i/32) (derivable from the
+// definition; the table-generation check lives in the tests).
+OXS_CONST_TABLE uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+// (1/c, ln c) and (1/c, log2 c) for the 16 subintervals of [0x3f330000, 2*0x3f330000).
+OXS_CONST_TABLE double kLogInvc[16] = {
+    0x1.661ec79f8f3bep+0, 0x1.571ed4aaf883dp+0, 0x1.49539f0f010bp+0,  0x1.3c995b0b80385p+0,
+    0x1.30d190c8864a5p+0, 0x1.25e227b0b8eap+0,  0x1.1bb4a4a1a343fp+0, 0x1.12358f08ae5bap+0,
+    0x1.0953f419900a7p+0, 0x1p+0,               0x1.e608cfd9a47acp-1, 0x1.ca4b31f026aap-1,
+    0x1.b2036576afce6p-1, 0x1.9c2d163a1aa2dp-1, 0x1.886e6037841edp-1, 0x1.767dcf5534862p-1,
+};
+OXS_CONST_TABLE double kLnLogc[16] = {
+    -0x1.57bf7808caadep-2, -0x1.2bef0a7c06ddbp-2, -0x1.01eae7f513a67p-2, -0x1.b31d8a68224e9p-3,
+    -0x1.6574f0ac07758p-3, -0x1.1aa2bc79c81p-3,   -0x1.a4e76ce8c0e5ep-4, -0x1.1973c5a611cccp-4,
+    -0x1.252f438e10c1ep-5, 0x0p+0,                0x1.aa5aa5df25984p-5,  0x1.c5e53aa362eb4p-4,
+    0x1.526e57720db08p-3,  0x1.bc2860d22477p-3,   0x1.1058bc8a07ee1p-2,  0x1.4043057b6ee09p-2,
+};
+OXS_CONST_TABLE double kLog2Logc[16] = {
+    -0x1.efec65b963019p-2, -0x1.b0b6832d4fca4p-2, -0x1.7418b0a1fb77bp-2, -0x1.39de91a6dcf7bp-2,
+    -0x1.01d9bf3f2b631p-2, -0x1.97c1d1b3b7afp-3,  -0x1.2f9e393af3c9fp-3, -0x1.960cbbf788d5cp-4,
+    -0x1.a6f9db6475fcep-5, 0x0p+0,                0x1.338ca9f24f53dp-4,  0x1.476a9543891bap-3,
+    0x1.e840b4ac4e4d2p-3,  0x1.40645f0c6651cp-2,  0x1.88e9c2c1b9ff8p-2,  0x1.ce0a44eb17bccp-2,
+};
+
+// expf: x*32/ln2 = k + r, exp(x) = 2^(k/32) * 2^(r/32), 2^(r/32) by a cubic.
+template <bool FUSED>
+OXS_HD float expf_t(float x) {
+  const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
+  const double kShift = 0x1.8p+52;
+  const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+  const double C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+  const double C2 = 0x1.62e42ff0c52d6p-1 / 32;
+  uint32_t ux = f2u(x);
+  uint32_t abstop = (ux >> 20) & 0x7ff;
+  if (abstop >= (f2u(88.0f) >> 20)) {
+    if (ux == 0xff800000u) return 0.0f;            // exp(-inf) = 0
+    if (abstop >= 0x7f8) return x + x;             // nan, +inf
+    if (x > 0x1.62e42ep6f) return u2f(0x7f800000u); // overflow -> +inf
+    if (x < -0x1.9fe368p6f) return 0.0f;           // underflow -> +0
+  }
+  double xd = (double)x;
+  double kd, r;
+  if (FUSED) {
+    // The fused build computes z = InvLn2N*x once per use, fused into both
+    // the rounding shift and the reduction.
+    kd = fma_d(kInvLn2N, xd, kShift);
+  } else {
+    double z = kInvLn2N * xd;
+    kd = z + kShift;
+  }
+  uint64_t ki = d2u(kd);
+  kd -= kShift;
+  if (FUSED) {
+    r = fma_d(kInvLn2N, xd, -kd);
+  } else {
+    double z = kInvLn2N * xd;
+    r = z - kd;
+  }
+  uint64_t t = kExp2Tab[ki % 32];
+  t += ki << 47;
+  double s = u2d(t);
+  double zz = mad<FUSED>(C0, r, C1);
+  double r2 = r * r;
+  double y = mad<FUSED>(C2, r, 1.0);
+  y = mad<FUSED>(zz, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// Shared argument reduction of logf/log2f: x = 2^k z, z in [OFF, 2 OFF).
+// Returns false (and sets *special) for zero, negative, inf, nan inputs.
+template <bool LOG2>
+OXS_HD bool log_special(float x, uint32_t* ix_io, float* special) {
+  uint32_t ix = *ix_io;
+  if (ix == 0x3f800000u) { *special = 0.0f; return true; }
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+    if (ix * 2 == 0) { *special = u2f(0xff800000u); return true; }         // -inf
+    if (ix == 0x7f800000u) { *special = x; return true; }                   // +inf
+    if ((ix & 0x80000000u) || ix * 2 >= 0xff000000u) {                      // nan
+      *special = u2f(0x7fc00000u);
+      if (ix * 2 > 0xff000000u) *special = x;
+      return true;
+    }
+    // subnormal: normalise
+    ix = f2u(x * 0x1p23f);
+    ix -= 23u << 23;
+  }
+  *ix_io = ix;
+  return false;
+}
+
+template <bool FUSED>
+OXS_HD float logf_t(float x) {
+  const double kLn2 = 0x1.62e42fefa39efp-1;
+  const double A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2, A2 = -0x1.ffffef20a4123p-2;
+  uint32_t ix = f2u(x);
+  float sp;
+  if (log_special<false>(x, &ix, &sp)) return sp;
+  uint32_t tmp = ix - 0x3f330000u;
+  int i = (int)((tmp >> (23 - 4)) % 16);
+  int k = (int32_t)tmp >> 23;
+  uint32_t iz = ix - (tmp & 0xff800000u);
+  double invc = kLogInvc[i], logc = kLnLogc[i];
+  double z = (double)u2f(iz);
+  double r = mad<FUSED>(z, invc, -1.0);
+  double y0 = mad<FUSED>((double)k, kLn2, logc);
+  double r2 = r * r;
+  double y = mad<FUSED>(A1, r, A2);
+  y = mad<FUSED>(A0, r2, y);
+  y = mad<FUSED>(y, r2, y0 + r);
+  return (float)y;
+}
+
+template <bool FUSED>
+OXS_HD float log2f_t(float x) {
+  const double A0 = -0x1.712b6f70a7e4dp-2, A1 = 0x1.ecabf496832ep-2, A2 = -0x1.715479ffae3dep-1,
+               A3 = 0x1.715475f35c8b8p0;
+  uint32_t ix = f2u(x);
+  float sp;
+  if (log_special<true>(x, &ix, &sp)) return sp;
+  uint32_t tmp = ix - 0x3f330000u;
+  int i = (int)((tmp >> (23 - 4)) % 16);
+  uint32_t top = tmp & 0xff800000u;
+  uint32_t iz = ix - top;
+  int k = (int32_t)tmp >> 23;
+  double invc = kLogInvc[i], logc = kLog2Logc[i];
+  double z = (double)u2f(iz);
+  double r = mad<FUSED>(z, invc, -1.0);
+  double y0 = logc + (double)k;
+  double r2 = r * r;
+  double y = mad<FUSED>(A1, r, A2);
+  y = mad<FUSED>(A0, r2, y);
+  double p = mad<FUSED>(A3, r, y0);
+  y = mad<FUSED>(y, r2, p);
+  return (float)y;
+}
+
+}  // namespace oxs_libm

@@ -1,0 +1,40 @@
+"""Python view of the MI355X batched token sampler (liboxide_sampler.so).
+
+Two layers, both thin over the C ABI in include/oxide_sampler.h:
+
+- `BatchSampler`: the batched device call, `oxs_sample_batch`, on torch
+  tensors that already live on the GPU (the decode-loop form).
+- `SamplingConfig`, `MirostatMode`, `SamplerState`, `AcademicSamplerEngine`:
+  the reference's single-row API (crates/oxide-core/src/sampler.rs:15-390),
+  same names and argument meaning, each call running one row on the GPU.
+
+There is no CPU path: without the built library every call raises
+`LibraryMissing`.
+"""
+from .engine import (
+    AcademicSamplerEngine,
+    BatchSampler,
+    MirostatMode,
+    SamplerState,
+    SamplingConfig,
+    ShapeMismatch,
+    configs_to_array,
+)
+from ._abi import (
+    LibraryMissing,
+    OxsError,
+    load_library,
+)
+
+__all__ = [
+    "AcademicSamplerEngine",
+    "BatchSampler",
+    "MirostatMode",
+    "SamplerState",
+    "SamplingConfig",
+    "ShapeMismatch",
+    "configs_to_array",
+    "LibraryMissing",
+    "OxsError",
+    "load_library",
+]

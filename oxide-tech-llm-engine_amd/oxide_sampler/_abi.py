@@ -1,0 +1,179 @@
+"""ctypes view of include/oxide_sampler.h (the C ABI of liboxide_sampler.so).
+
+The structures mirror the header field for field; `check_layout()` compares
+their sizes with the C definitions compiled into the library's tests.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent.parent  # oxide-tech-llm-engine_amd/
+LIB_PATH = PKG_ROOT / "lib" / "liboxide_sampler.so"
+
+OXS_ABI_VERSION = 1
+
+OXS_OK = 0
+OXS_ERR_INVALID_ARGUMENT = -1
+OXS_ERR_SHAPE_MISMATCH = -2
+OXS_ERR_LIMITS = -3
+OXS_ERR_HIP = -4
+OXS_ERR_UNSUPPORTED = -5
+OXS_ERR_NO_DEVICE = -6
+
+OXS_ROW_OK = 0
+OXS_ROW_EMPTY = 1
+OXS_ROW_HISTORY_FULL = 2
+OXS_ROW_UNSUPPORTED = 3
+OXS_ROW_MISSING_STATE = 4
+
+OXS_MIROSTAT_DISABLED = 0
+OXS_MIROSTAT_V1 = 1
+OXS_MIROSTAT_V2 = 2
+
+OXS_DTYPE_F32 = 0
+OXS_DTYPE_BF16 = 1
+
+OXS_FLAG_RECORD_HISTORY = 1
+OXS_FLAG_SHARED_CONFIG = 2
+
+# Exported symbols declared in include/oxide_sampler.h.
+EXPORTED_SYMBOLS = (
+    "oxs_abi_version",
+    "oxs_status_string",
+    "oxs_sampling_config_default",
+    "oxs_rng_state_from_seed",
+    "oxs_mirostat_mu_from_tau",
+    "oxs_sampler_create",
+    "oxs_sampler_destroy",
+    "oxs_sampler_workspace_bytes",
+    "oxs_sample_batch",
+)
+
+
+class OxsSamplingConfig(ctypes.Structure):
+    _fields_ = [
+        ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_uint32),
+        ("top_p", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("tfs_z", ctypes.c_float),
+        ("typical_p", ctypes.c_float),
+        ("xtc_threshold", ctypes.c_float),
+        ("xtc_probability", ctypes.c_float),
+        ("mirostat_mode", ctypes.c_int32),
+        ("mirostat_tau", ctypes.c_float),
+        ("mirostat_eta", ctypes.c_float),
+        ("dry_multiplier", ctypes.c_float),
+        ("dry_base", ctypes.c_float),
+        ("dry_allowed_length", ctypes.c_uint32),
+        ("dry_range", ctypes.c_uint32),
+        ("repeat_penalty", ctypes.c_float),
+        ("repeat_last_n", ctypes.c_uint32),
+        ("frequency_penalty", ctypes.c_float),
+        ("presence_penalty", ctypes.c_float),
+        ("penalize_nl", ctypes.c_uint32),
+        ("newline_penalty", ctypes.c_float),
+        ("newline_token_id", ctypes.c_uint32),
+        ("bias_offset", ctypes.c_uint32),
+        ("bias_count", ctypes.c_uint32),
+        ("ban_offset", ctypes.c_uint32),
+        ("ban_count", ctypes.c_uint32),
+    ]
+
+
+class OxsLimits(ctypes.Structure):
+    _fields_ = [
+        ("max_batch", ctypes.c_uint32),
+        ("max_vocab", ctypes.c_uint32),
+        ("max_top_k", ctypes.c_uint32),
+    ]
+
+
+class OxsBatch(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_uint32),
+        ("vocab", ctypes.c_uint32),
+        ("logits_dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+        ("logits_ld", ctypes.c_int64),
+        ("logits", ctypes.c_void_p),
+        ("configs", ctypes.c_void_p),
+        ("bias_ids", ctypes.c_void_p),
+        ("bias_values", ctypes.c_void_p),
+        ("ban_ids", ctypes.c_void_p),
+        ("allowed_mask", ctypes.c_void_p),
+        ("mask_ld", ctypes.c_int64),
+        ("history", ctypes.c_void_p),
+        ("history_ld", ctypes.c_int64),
+        ("history_len", ctypes.c_void_p),
+        ("history_cap", ctypes.c_uint32),
+        ("uniforms", ctypes.c_void_p),
+        ("rng_state", ctypes.c_void_p),
+        ("mirostat_mu", ctypes.c_void_p),
+        ("out_tokens", ctypes.c_void_p),
+        ("out_status", ctypes.c_void_p),
+        ("out_kept_count", ctypes.c_void_p),
+        ("out_kept_ids", ctypes.c_void_p),
+        ("out_kept_probs", ctypes.c_void_p),
+        ("kept_ld", ctypes.c_int64),
+        ("logits_out", ctypes.c_void_p),
+        ("logits_out_ld", ctypes.c_int64),
+    ]
+
+
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    """Raised when liboxide_sampler.so has not been built: there is no fallback."""
+
+
+def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """Loads liboxide_sampler.so and declares its prototypes. Fails loudly."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise LibraryMissing(
+            f"{p} is not built; run `make -C oxide-tech-llm-engine_amd` or "
+            "`python -c 'import __graft_entry__; __graft_entry__.build()'`")
+    lib = ctypes.CDLL(str(p))
+    lib.oxs_abi_version.restype = ctypes.c_uint32
+    lib.oxs_abi_version.argtypes = []
+    lib.oxs_status_string.restype = ctypes.c_char_p
+    lib.oxs_status_string.argtypes = [ctypes.c_int]
+    lib.oxs_sampling_config_default.restype = None
+    lib.oxs_sampling_config_default.argtypes = [ctypes.POINTER(OxsSamplingConfig)]
+    lib.oxs_rng_state_from_seed.restype = ctypes.c_uint64
+    lib.oxs_rng_state_from_seed.argtypes = [ctypes.c_int, ctypes.c_uint64]
+    lib.oxs_mirostat_mu_from_tau.restype = ctypes.c_float
+    lib.oxs_mirostat_mu_from_tau.argtypes = [ctypes.c_float]
+    lib.oxs_sampler_create.restype = ctypes.c_int
+    lib.oxs_sampler_create.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(OxsLimits), ctypes.c_int]
+    lib.oxs_sampler_destroy.restype = ctypes.c_int
+    lib.oxs_sampler_destroy.argtypes = [ctypes.c_void_p]
+    lib.oxs_sampler_workspace_bytes.restype = ctypes.c_size_t
+    lib.oxs_sampler_workspace_bytes.argtypes = [ctypes.c_void_p]
+    lib.oxs_sample_batch.restype = ctypes.c_int
+    lib.oxs_sample_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.c_void_p]
+    if lib.oxs_abi_version() != OXS_ABI_VERSION:
+        raise RuntimeError(f"liboxide_sampler ABI {lib.oxs_abi_version()} != {OXS_ABI_VERSION}")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+class OxsError(RuntimeError):
+    def __init__(self, code: int, what: str = ""):
+        self.code = code
+        lib = _lib
+        text = lib.oxs_status_string(code).decode() if lib is not None else str(code)
+        super().__init__(f"{what}: {text} ({code})" if what else f"{text} ({code})")
+
+
+def check(code: int, what: str = "") -> None:
+    if code != OXS_OK:
+        raise OxsError(code, what)
