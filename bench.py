@@ -1,0 +1,299 @@
+#!/usr/bin/env python3
+"""bench.py — throughput of the MI355X batched token sampler.
+
+Metric: sampled rows/s and achieved HBM GB/s for the full
+sampling chain at batch 64 x vocab 128256, fp32 logits (config 2: frequency
+0.3 + presence 0.2 + repetition 1.05 over a 512-token history -> temperature
+0.7 -> top-k 50 -> top-p 0.9 -> min-p 0.05 -> draw with a supplied uniform).
+
+One step = one `oxs_sample_batch` launch over one batch of 64 rows. Inputs are
+resident in HBM before timing. Steps rotate over a pool of distinct batches
+larger than twice the 256 MiB Infinity Cache, so the logits come from HBM.
+Launches are replayed from a captured HIP graph (the decode-loop form: a
+host-side Python loop cannot issue launches as fast as the GPU runs them).
+
+Prints one JSON line (see `main`). `--gpus N` with N > 1 exits: this build
+runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "oxide-tech-llm-engine_amd"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def algorithmic_bytes(B, V, H, kept_avg, esz=4, mask_words=0):
+    """Bytes a perfect single pass must move per launch (reads + writes)."""
+    per_row = V * esz + H * 4 + mask_words * 4 + 4 + 4 + 4 + 4 + kept_avg * 8 + 104
+    return B * per_row
+
+
+def make_pool(torch, w, n_pool, seed=0x5EED0002):
+    """Pool entry 0 is the seeded CPU workload; the rest are drawn on the GPU
+    from the same distribution (N(0,3) + -1.1 ln(rank) over a random permutation)."""
+    d = torch.device("cuda")
+    B, V = w.batch, w.vocab
+    pool = [torch.from_numpy(np.ascontiguousarray(w.logits)).to(d)]
+    g = torch.Generator(device=d)
+    g.manual_seed(seed)
+    prior = (-1.1 * torch.log(torch.arange(1, V + 1, device=d, dtype=torch.float64))).to(torch.float32)
+    for _ in range(1, n_pool):
+        x = torch.randn(B, V, device=d, generator=g) * 3.0
+        perm = torch.argsort(torch.rand(B, V, device=d, generator=g), dim=1)
+        x += prior[perm]
+        pool.append(x.contiguous())
+    return pool
+
+
+def cpu_baseline(w, gpu_tokens, seconds):
+    """The CPU oracle (a restatement of sampler.rs) on this host, 1 thread, rows
+    in series as the reference decode loop does, over a bounded sample."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oxs_oracle_ctypes as oracle  # noqa: PLC0415 — baseline leg only
+    from oxide_sampler import _abi  # noqa: PLC0415
+
+    oracle.load()
+    cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
+
+    def run(rows, n_threads=1):
+        hist = w.history[:rows].copy()
+        hlen = w.history_len[:rows].copy()
+        return oracle.sample_batch_host(
+            _abi, logits=np.ascontiguousarray(w.logits[:rows]), dtype=w.dtype, configs_bytes=cfg,
+            bias_ids=bias_ids, bias_values=bias_vals, ban_ids=ban_ids, mask=None, history=hist, history_len=hlen,
+            history_cap=hist.shape[1], record=False, uniforms=w.uniforms[:rows], rng_state=None, mu=None,
+            kept_ld=64, n_threads=n_threads)
+
+    t0 = time.perf_counter()
+    out = run(w.batch)  # warm-up and parity spot check on the whole batch
+    t_batch = time.perf_counter() - t0
+    match = bool(np.array_equal(out["tokens"], gpu_tokens))
+    reps = max(1, int(seconds / max(t_batch, 1e-6)))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run(w.batch)
+    dt = time.perf_counter() - t0
+    rows = reps * w.batch
+    ncores = len(os.sched_getaffinity(0))
+    t0 = time.perf_counter()
+    run(w.batch, n_threads=min(ncores, w.batch))
+    dt_all = time.perf_counter() - t0
+    cpu_model = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": rows / dt,
+        "unit": "rows/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{rows} rows ({reps} passes over config-2 batch 0: B=64, V=128256 f32), 1 thread, rows in series",
+        "us_per_row": dt / rows * 1e6,
+        "all_cores": {"value": w.batch / dt_all, "unit": "rows/s", "cores": min(ncores, w.batch),
+                      "sample": "one pass over config-2 batch 0, rows split statically"},
+        "cpu_model": cpu_model,
+        "libc": " ".join(platform.libc_ver()),
+        "tokens_match_gpu": match,
+    }
+
+
+def read_traffic(path):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    try:
+        data = json.loads(Path(path).read_text())
+        return float(data["traffic_bytes_per_launch"]), str(path)
+    except Exception:
+        return None, None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=8000)
+    ap.add_argument("--warmup", type=int, default=800)
+    ap.add_argument("--pool", type=int, default=16, help="distinct input batches (16 x 32.8 MB > 2 x 256 MiB)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch from a Python loop instead of a HIP graph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only 8 plain 256 MiB device copies (scale for the rocprofv3 byte counters)")
+    ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build samples on one GPU; multi-GPU runs are not part of it "
+              "(rows shard across GPUs with no communication, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from oxide_sampler import BatchSampler, _abi
+    from oxide_sampler import workloads as wl
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+    d = torch.device("cuda")
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=d)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": src.numel() * 4, "copies": 8}), flush=True)
+        return
+    w = wl.config2()
+    B, V = w.batch, w.vocab
+    H = int(w.history_len[0])
+    pool = make_pool(torch, w, args.pool)
+    cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
+    d_cfg = torch.from_numpy(cfg).to(d)
+    d_hist = torch.from_numpy(w.history.view(np.int32).copy()).to(d)
+    d_hlen = torch.from_numpy(w.history_len.view(np.int32).copy()).to(d)
+    d_u = torch.from_numpy(w.uniforms).to(d)
+    kept_ld = 64
+    sampler = BatchSampler(B, V, 256)
+
+    # One prepared descriptor per pool entry; outputs are shared.
+    outs = {
+        "tokens": torch.empty(B, dtype=torch.int32, device=d),
+        "status": torch.empty(B, dtype=torch.int32, device=d),
+        "kept_count": torch.empty(B, dtype=torch.int32, device=d),
+        "kept_ids": torch.empty(B, kept_ld, dtype=torch.int32, device=d),
+        "kept_probs": torch.empty(B, kept_ld, dtype=torch.float32, device=d),
+    }
+    descs = []
+    for x in pool:
+        b = _abi.OxsBatch()
+        b.batch, b.vocab, b.logits_dtype, b.flags = B, V, _abi.OXS_DTYPE_F32, 0
+        b.logits_ld, b.logits, b.configs = V, x.data_ptr(), d_cfg.data_ptr()
+        b.history, b.history_ld, b.history_len, b.history_cap = d_hist.data_ptr(), d_hist.stride(0), d_hlen.data_ptr(), 0
+        b.uniforms = d_u.data_ptr()
+        b.out_tokens, b.out_status = outs["tokens"].data_ptr(), outs["status"].data_ptr()
+        b.out_kept_count = outs["kept_count"].data_ptr()
+        b.out_kept_ids, b.out_kept_probs, b.kept_ld = outs["kept_ids"].data_ptr(), outs["kept_probs"].data_ptr(), kept_ld
+        descs.append(b)
+
+    # Eager outputs of the last pool entry (checked against the graph replay)
+    # and of entry 0 (checked against the CPU oracle in the baseline leg).
+    P = len(descs)
+    sampler.launch(descs[P - 1])
+    torch.cuda.synchronize()
+    tokens_last = outs["tokens"].cpu().numpy().view(np.uint32).copy()
+    sampler.launch(descs[0])
+    torch.cuda.synchronize()
+    tokens0 = outs["tokens"].cpu().numpy().view(np.uint32).copy()
+    kept_avg = float(outs["kept_count"].float().mean().item())
+    assert (outs["status"] == 0).all().item(), "sampler reported a non-OK row status"
+
+    stream = torch.cuda.Stream()
+    mode = "eager"
+    graph = None
+    if not args.eager:
+        try:
+            stream.wait_stream(torch.cuda.current_stream())
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(P):
+                    sampler.launch(descs[i])
+            torch.cuda.synchronize()
+            mode = "hip_graph"
+        except Exception as e:  # fall back to eager launches, and say so
+            print(f"bench.py: graph capture failed ({e}); timing eager launches", file=sys.stderr)
+            graph = None
+
+    def run_steps(n):
+        """n launches (n a multiple of P in graph mode)."""
+        with torch.cuda.stream(stream):
+            if graph is not None:
+                for _ in range(n // P):
+                    graph.replay()
+            else:
+                for i in range(n):
+                    sampler.launch(descs[i % P], stream)
+
+    steps = args.steps if graph is None else max(P, (args.steps + P - 1) // P * P)
+    warm = args.warmup if graph is None else max(P, (args.warmup + P - 1) // P * P)
+    run_steps(warm)
+    torch.cuda.synchronize()
+    if graph is not None:  # a replay ends with pool entry P-1: same tokens as eager
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(outs["tokens"].cpu().numpy().view(np.uint32), tokens_last), \
+            "graph replay differs from the eager launch"
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    t0 = time.perf_counter()
+    run_steps(steps)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    elapsed_ms = ev0.elapsed_time(ev1)
+    ms_per_step = elapsed_ms / steps
+    rows_per_s = B * steps / (elapsed_ms / 1e3)
+
+    alg = algorithmic_bytes(B, V, H, kept_avg)
+    achieved = alg / (ms_per_step / 1e3) / 1e9
+    traffic, traffic_src = read_traffic(args.traffic_summary)
+    result = {
+        "metric": "sampled rows/sec + achieved HBM GB/s, batch 64 x 128256 vocab full chain",
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded config-2 batch + 15 GPU-drawn batches of the same distribution)",
+        "config": {
+            "workload": "config2: B=64 x V=128256 f32 logits, history 512; freq 0.3 + presence 0.2 + repeat 1.05 "
+                        "-> temp 0.7 -> top-k 50 -> top-p 0.9 -> min-p 0.05 -> draw with supplied u",
+            "batch": B, "vocab": V, "history": H, "pool_batches": P,
+            "pool_bytes": P * B * V * 4, "launch": mode,
+        },
+        "tokens_per_s": rows_per_s,
+        "achieved_GBps": achieved,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": alg,
+            "traffic_source": traffic_src,
+            "kernel": "oxs::sample_kernel<0,8,true>",
+        },
+        "wall_s": wall,
+    }
+    if achieved > 1.05 * HBM_PEAK_GBS:  # roofline.rs:53-style integrity check
+        result["roofline"]["warning"] = "achieved exceeds 1.05 x peak: inputs were cached, not streamed"
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(w, tokens0, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

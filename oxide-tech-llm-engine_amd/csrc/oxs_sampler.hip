@@ -1,28 +1,33 @@
 // oxs_sampler.hip — batched token sampler for MI355X (gfx950).
 //
 // Replaces the per-row CPU chain of crates/oxide-core/src/sampler.rs
-// (AcademicSamplerEngine::sample_token, sampler.rs:173-390) with one kernel
-// launch per batch. The launch has two roles:
+// (AcademicSamplerEngine::sample_token, sampler.rs:173-390) with two kernels
+// per batch, launched back to back on the caller's stream:
 //
-// Phase A (every block): block (row, chunk) streams CH logits of one row with
-//   coalesced 16-byte loads, applies the grammar mask, bans, biases, newline,
-//   repetition/frequency/presence penalties and temperature in registers (in the
-//   reference's order, with the reference's IEEE operations), and keeps only a
-//   small candidate set: each wavefront finds the c-th largest of its 64 lane
-//   maxima (32 ballot steps) and writes every element at or above it as a
-//   64-bit key (order-preserving value bits << 32 | ~token id). Keys are unique
-//   and order candidates by value descending, then by lower token id.
+// stream_kernel (grid: rows x chunks). Each block streams CH logits of one row
+//   with coalesced 16-byte loads and keeps only a small candidate set per
+//   wavefront. Dense stages (mask, temperature) are applied in registers. The
+//   sparse stages (bans, biases, newline, repetition/frequency/presence over
+//   the history window) touch few ids; the block marks those ids in an LDS
+//   bitmap, leaves them out of the stream, and computes their exact values in
+//   a short pass at the end. Each wavefront finds the c-th largest of its 64
+//   lane maxima (32 ballot steps) and writes every unmarked element at or above
+//   it, plus its share of the marked ones, as 64-bit keys
+//   (order-preserving value bits << 32 | ~token id): keys are unique and order
+//   candidates by value descending, then lower token id.
 //
-// Tail (the last block of each row, chosen by an atomic ticket): gathers the
-//   row's candidate sets, selects the exact top M = max(top_k, 256) by radix
-//   select, checks that every wavefront's threshold lies at or below the M-th
-//   key (which proves the union holds the row's true top M; otherwise the block
-//   re-scans the row exactly), sorts the M keys, and runs softmax, Mirostat or
-//   min-p / XTC / top-k / tail-free / typical / top-p, renormalisation and the
-//   inverse-CDF draw, using expf/logf/log2f that reproduce glibc bit for bit.
+// tail_kernel (one block per row). Reads the row's candidate keys and the
+//   wavefront thresholds; if at least M = max(top_k, 256) keys lie at or above
+//   the largest threshold, those keys provably contain the row's top M
+//   (otherwise the block re-scans the row exactly). A bucketed counting sort
+//   yields the sorted top M, then softmax, Mirostat or min-p / XTC / top-k /
+//   tail-free / typical / top-p, renormalisation and the inverse-CDF draw run
+//   with expf/logf/log2f that reproduce glibc bit for bit and with every float
+//   sum in the reference's order.
 //
-// No allocation, no host synchronisation; all workspace comes from the sampler
-// handle.
+// The kernel boundary makes the candidate keys visible to the tail on every
+// XCD without per-block cache write-backs. Nothing is allocated and nothing
+// waits on the host; all workspace comes from the sampler handle.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -35,10 +40,13 @@ namespace oxs {
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / 64;
-constexpr int kUnionMax = 4096;   // candidate keys a row's tail can hold
+constexpr int kUnionMax = 4096;   // candidate keys per row (tail LDS)
 constexpr int kMaxM = 1024;       // largest max(top_k, 256) run on the device
-constexpr int kMaxChunk = 8192;   // logits per block (size of the LDS penalty table)
-constexpr int kMaxChunks = 64;    // chunks per row (4 wavefronts each -> <= 256 tail entries)
+constexpr int kMaxChunk = 8192;   // logits per stream block
+constexpr int kMaxChunks = 64;    // chunks per row
+constexpr int kHashSlots = 256;   // marked (sparse-stage) ids per stream block
+constexpr int kBuckets = 1024;    // tail counting-sort buckets
+constexpr int kHistUnroll = 4;    // history ids per thread loaded ahead of the stream
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -46,6 +54,7 @@ constexpr uint32_t kCountMask = 0x0fffffffu;
 constexpr uint32_t kBanFlag = 1u << 28;
 constexpr uint32_t kBiasFlag = 1u << 29;
 constexpr uint32_t kNlFlag = 1u << 30;
+constexpr uint32_t kEmpty = 0xffffffffu;
 
 struct Params {
   const void* logits;
@@ -73,17 +82,16 @@ struct Params {
   float* logits_out;
   int64_t logits_out_ld;
   // geometry
-  uint32_t S;          // chunks per row
-  uint32_t CH;         // logits per chunk
-  uint32_t cap_w;      // key slots per wavefront
-  uint32_t c_w;        // lane maxima per wavefront that set its threshold
-  uint32_t grid_real;  // B * S
-  uint32_t grid_per_xcd;
+  uint32_t S;      // chunks per row
+  uint32_t CH;     // logits per chunk
+  uint32_t cap_w;  // key slots per wavefront (a power of two)
+  uint32_t cap_shift;  // log2(cap_w)
+  uint32_t c_w;    // lane maxima per wavefront that set its threshold
+  uint32_t rpx;    // rows per XCD when rows are grouped by XCD, else 0
   // workspace
   uint64_t* lists;       // [B][S*4][cap_w]
   uint64_t* wave_theta;  // [B][S*4]
   uint32_t* wave_count;  // [B][S*4]
-  uint32_t* tickets;     // [B]
 };
 
 // ---------------------------------------------------------------- keys
@@ -105,6 +113,14 @@ __device__ __forceinline__ float ord2f(uint32_t o) {
 __device__ __forceinline__ uint32_t cand_key(float x) { return (x > neg_inf()) ? f2ord(x) : 0u; }
 __device__ __forceinline__ uint64_t comp_key(uint32_t k, uint32_t idx) {
   return ((uint64_t)k << 32) | (uint64_t)(~idx);
+}
+
+// Row index of a block under the XCD grouping: the hardware hands workgroups
+// to the 8 XCDs round robin, so block i runs on XCD i % 8. With rpx > 0, XCD x
+// owns rows [x * rpx, (x + 1) * rpx): the stream blocks and the tail block of a
+// row then share one L2.
+__device__ __forceinline__ uint32_t grouped_index(uint32_t block, uint32_t per_xcd) {
+  return (block & 7u) * per_xcd + (block >> 3);
 }
 
 // ---------------------------------------------------------------- row setup
@@ -146,97 +162,48 @@ __device__ __forceinline__ RowXf make_row_xf(const Params& p, const oxs_sampling
   return r;
 }
 
-// The sparse pre-softmax stages for one flagged logit, in reference order:
+// The sparse pre-softmax stages for one marked logit, in reference order:
 // ban (:184-188), bias (:189-193), newline (:196-200), repetition (:217-229),
 // frequency/presence (:232-245). Temperature is applied by the caller.
-__device__ __noinline__ float apply_special(const Params& p, const RowXf& r, float x,
-                                            uint32_t entry, uint32_t idx) {
+__device__ __forceinline__ float apply_special(const uint32_t* bias_ids, const float* bias_values,
+                                               const RowXf& r, float x, uint32_t entry,
+                                               uint32_t idx) {
   if (entry & kBanFlag) x = neg_inf();
   if (entry & kBiasFlag) {
     float b = 0.0f;
-    for (uint32_t k = 0; k < r.bias_cnt; ++k)  // last entry for an id wins (HashMap::insert)
-      if (p.bias_ids[r.bias_off + k] == idx) b = p.bias_values[r.bias_off + k];
+    for (uint32_t k = 0; k < r.bias_cnt; ++k)  // the last entry for an id wins (HashMap::insert)
+      if (bias_ids[r.bias_off + k] == idx) b = bias_values[r.bias_off + k];
     x += b;
   }
   if (entry & kNlFlag) x -= r.nl_pen;
-  uint32_t cnt = entry & kCountMask;
+  const uint32_t cnt = entry & kCountMask;
   if (cnt) {
     if (r.pen_rep) x = (x > 0.0f) ? x / r.rp : x * r.rp;
     if (r.pen_fp) {
-      float t = (float)cnt * r.fp;
-      float pen = t + r.pp;
+      const float t = (float)cnt * r.fp;
+      const float pen = t + r.pp;
       x = x - pen;
     }
   }
   return x;
 }
 
-// Builds the penalty table of logits [c0, c1): window counts in the low bits,
-// ban/bias/newline flags in the high bits. Ends with a barrier.
-__device__ void build_table(const Params& p, const RowXf& r, uint32_t row, uint32_t c0,
-                            uint32_t c1, uint32_t* table) {
-  const uint32_t tid = threadIdx.x;
-  const uint32_t n = c1 - c0;
-  for (uint32_t i = tid * 4; i < n; i += kThreads * 4) {
-    *(uint4*)(table + i) = make_uint4(0, 0, 0, 0);
-  }
-  __syncthreads();
-  if (r.use_hist) {
-    const uint32_t* h = p.history + (size_t)row * p.history_ld + r.wstart;
-    for (uint32_t j = tid; j < r.wn; j += kThreads) {
-      uint32_t t = h[j];
-      if (t >= c0 && t < c1) atomicAdd(&table[t - c0], 1u);
-    }
-  }
-  for (uint32_t k = tid; k < r.ban_cnt; k += kThreads) {
-    uint32_t id = p.ban_ids[r.ban_off + k];
-    if (id >= c0 && id < c1) atomicOr(&table[id - c0], kBanFlag);
-  }
-  for (uint32_t k = tid; k < r.bias_cnt; k += kThreads) {
-    uint32_t id = p.bias_ids[r.bias_off + k];
-    if (id >= c0 && id < c1) atomicOr(&table[id - c0], kBiasFlag);
-  }
-  if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1) atomicOr(&table[r.nl_id - c0], kNlFlag);
-  __syncthreads();
-}
-
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
-// One logit, scalar path (ragged tails and the exact re-scan).
 template <int DT>
 __device__ __forceinline__ float load_logit(const Params& p, uint32_t row, uint32_t idx) {
-  if (DT == OXS_DTYPE_F32) {
+  if constexpr (DT == OXS_DTYPE_F32) {
     return ((const float*)p.logits)[(size_t)row * p.ld + idx];
   } else {
-    uint16_t b = ((const uint16_t*)p.logits)[(size_t)row * p.ld + idx];
+    const uint16_t b = ((const uint16_t*)p.logits)[(size_t)row * p.ld + idx];
     return __uint_as_float((uint32_t)b << 16);
   }
 }
 
 __device__ __forceinline__ bool mask_allows(const Params& p, uint32_t row, uint32_t idx) {
-  uint32_t w = p.mask[(size_t)row * p.mask_ld + (idx >> 5)];
+  const uint32_t w = p.mask[(size_t)row * p.mask_ld + (idx >> 5)];
   return (w >> (idx & 31)) & 1u;
 }
 
-// Full pre-softmax transform of one logit (scalar path).
-template <int DT>
-__device__ __forceinline__ float transformed_logit(const Params& p, const RowXf& r, uint32_t row,
-                                                   uint32_t idx, uint32_t c0,
-                                                   const uint32_t* table) {
-  float x = load_logit<DT>(p, row, idx);
-  if (p.mask && !mask_allows(p, row, idx)) x = neg_inf();
-  if (r.any_special) {
-    uint32_t e = table[idx - c0];
-    if (e) x = apply_special(p, r, x, e, idx);
-  }
-  if (r.do_temp) x *= r.inv_temp;
-  return x;
-}
-
 // ---------------------------------------------------------------- block helpers
-
-struct TailShared;  // fwd
 
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 #pragma unroll
@@ -250,7 +217,7 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scrat
   uint32_t x = v;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    uint32_t y = __shfl_up(x, o, 64);
+    const uint32_t y = __shfl_up(x, o, 64);
     if (lane >= (uint32_t)o) x += y;
   }
   if (lane == 63) scratch[w] = x;
@@ -258,7 +225,7 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scrat
   uint32_t before = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < kWavesPerBlock; ++i) {
-    uint32_t s = scratch[i];
+    const uint32_t s = scratch[i];
     if ((uint32_t)i < w) before += s;
     tot += s;
   }
@@ -267,94 +234,295 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scrat
   return x - v + before;
 }
 
-__device__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch) {
+template <bool MAX>
+__device__ uint64_t block_reduce_u64(uint64_t v, uint64_t* scratch) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    uint64_t y = __shfl_xor(v, o, 64);
-    v = y > v ? y : v;
+    const uint64_t y = __shfl_xor(v, o, 64);
+    v = MAX ? (y > v ? y : v) : (y < v ? y : v);
   }
   if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
   __syncthreads();
   uint64_t m = scratch[0];
 #pragma unroll
-  for (int i = 1; i < kWavesPerBlock; ++i) m = scratch[i] > m ? scratch[i] : m;
+  for (int i = 1; i < kWavesPerBlock; ++i) m = MAX ? (scratch[i] > m ? scratch[i] : m) : (scratch[i] < m ? scratch[i] : m);
   __syncthreads();
   return m;
 }
 
-__device__ uint64_t block_min_u64(uint64_t v, uint64_t* scratch) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t y = __shfl_xor(v, o, 64);
-    v = y < v ? y : v;
+// ---------------------------------------------------------------- marked-id hash (LDS)
+
+__device__ __forceinline__ uint32_t hash_slot(uint32_t key) { return (key * 0x9e3779b1u) >> 24; }
+static_assert(kHashSlots == 256, "hash_slot yields 8 bits");
+
+// Inserts `key` (a chunk-local offset), adding `add` and OR-ing `orv` into its
+// value; false when the table is full.
+__device__ bool hash_insert(uint32_t* hkeys, uint32_t* hvals, uint32_t key, uint32_t add,
+                            uint32_t orv) {
+  uint32_t h = hash_slot(key);
+  for (int probe = 0; probe < kHashSlots; ++probe) {
+    const uint32_t prev = atomicCAS(&hkeys[h], kEmpty, key);
+    if (prev == kEmpty || prev == key) {
+      if (add) atomicAdd(&hvals[h], add);
+      if (orv) atomicOr(&hvals[h], orv);
+      return true;
+    }
+    h = (h + 1) & (kHashSlots - 1);
   }
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint64_t m = scratch[0];
-#pragma unroll
-  for (int i = 1; i < kWavesPerBlock; ++i) m = scratch[i] < m ? scratch[i] : m;
-  __syncthreads();
-  return m;
+  return false;
 }
+
+__device__ __forceinline__ int hash_find(const uint32_t* hkeys, uint32_t key) {
+  uint32_t h = hash_slot(key);
+  for (int probe = 0; probe < kHashSlots; ++probe) {
+    const uint32_t k = hkeys[h];
+    if (k == key) return (int)h;
+    if (k == kEmpty) return -1;
+    h = (h + 1) & (kHashSlots - 1);
+  }
+  return -1;
+}
+
+// Marks one chunk-local id.
+__device__ __forceinline__ bool mark(uint32_t* bitmap, uint32_t* hkeys, uint32_t* hvals,
+                                     uint32_t off, uint32_t add, uint32_t orv) {
+  atomicOr(&bitmap[off >> 5], 1u << (off & 31));
+  return hash_insert(hkeys, hvals, off, add, orv);
+}
+
+// ---------------------------------------------------------------- stream kernel
+
+constexpr uint32_t kMinValidOrd = 0x00800000u;  // f2ord(-FLT_MAX): every candidate key is >= this
+constexpr uint64_t kAllValid = (uint64_t)kMinValidOrd << 32;  // threshold of a wavefront that kept all
+
+template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
+__global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
+  constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;  // logits per 16-byte load
+  constexpr int TILE = kThreads * EPL;
+  constexpr int CH = SLOTS * TILE;
+  constexpr int NE = SLOTS * EPL;  // logits per lane
+  constexpr size_t ESZ = (DT == OXS_DTYPE_F32) ? 4 : 2;
+  static_assert(CH <= kMaxChunk, "chunk too large");
+  static_assert(NE <= 32, "one survivor bit per logit of a lane");
+
+  __shared__ __align__(16) float s_x[CH];  // the chunk's masked raw logits
+  __shared__ uint32_t s_bitmap[CH / 32];  // marked (sparse-stage) ids
+  __shared__ uint32_t s_hkeys[kHashSlots];
+  __shared__ uint32_t s_hvals[kHashSlots];
+  __shared__ uint32_t s_wcount[kWavesPerBlock];
+  __shared__ uint32_t s_wover[kWavesPerBlock];
+  __shared__ uint32_t s_wtheta[kWavesPerBlock];
+  __shared__ uint32_t s_full;
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63;
+  const uint32_t wave = tid >> 6;
+  uint32_t row, chunk;
+  if (p.rpx) {
+    const uint32_t v = grouped_index(blockIdx.x, p.rpx * p.S);
+    row = v / p.S;
+    chunk = v - row * p.S;
+  } else {
+    row = blockIdx.x / p.S;
+    chunk = blockIdx.x - row * p.S;
+  }
+  if (row >= p.B) return;
+  const oxs_sampling_config c = p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
+  const RowXf r = make_row_xf(p, c, row);
+  const uint32_t c0 = chunk * CH;
+  const uint32_t c1 = min(c0 + (uint32_t)CH, p.V);
+
+  // ---- 1. the chunk's logits and mask words, then the history window ids
+  uint32_t raw[SLOTS][EPL];
+  const char* rowp = (const char*)p.logits + (size_t)row * (size_t)p.ld * ESZ;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const uint32_t base = c0 + s * TILE + tid * EPL;
+    if constexpr (VEC) {
+      // V is a multiple of EPL here: past-the-end groups re-read the row's
+      // last group (in bounds) and their values are dropped below.
+      const uint32_t at = base < c1 ? base : p.V - EPL;
+      const u32x4 q = __builtin_nontemporal_load((const u32x4*)(rowp + (size_t)at * ESZ));
+      if constexpr (DT == OXS_DTYPE_F32) {
+        raw[s][0] = q.x; raw[s][1] = q.y; raw[s][2] = q.z; raw[s][3] = q.w;
+      } else {
+        raw[s][0] = q.x << 16; raw[s][1] = q.x & 0xffff0000u;
+        raw[s][2] = q.y << 16; raw[s][3] = q.y & 0xffff0000u;
+        raw[s][4] = q.z << 16; raw[s][5] = q.z & 0xffff0000u;
+        raw[s][6] = q.w << 16; raw[s][7] = q.w & 0xffff0000u;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const uint32_t idx = base + e;
+        raw[s][e] = __float_as_uint(load_logit<DT>(p, row, idx < c1 ? idx : p.V - 1));
+      }
+    }
+  }
+  uint32_t mw[SLOTS];
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    if constexpr (MASK) {
+      const uint32_t base = c0 + s * TILE + tid * EPL;
+      const uint32_t at = base < c1 ? base : p.V - 1;
+      mw[s] = p.mask[(size_t)row * p.mask_ld + (at >> 5)];
+    } else {
+      mw[s] = 0xffffffffu;
+    }
+  }
+  uint32_t hv[kHistUnroll];
+  const uint32_t* hrow = p.history + (size_t)row * p.history_ld + r.wstart;
+#pragma unroll
+  for (int q = 0; q < kHistUnroll; ++q) {
+    const uint32_t j = tid + q * kThreads;
+    hv[q] = (r.use_hist && j < r.wn) ? hrow[j] : kEmpty;
+  }
+
+  if (lane == 0) {
+    s_wcount[wave] = 0;
+    s_wover[wave] = 0;
+  }
+  if (r.any_special) {
+    for (uint32_t i = tid; i < (uint32_t)CH / 32; i += kThreads) s_bitmap[i] = 0;
+    for (uint32_t i = tid; i < (uint32_t)kHashSlots; i += kThreads) {
+      s_hkeys[i] = kEmpty;
+      s_hvals[i] = 0;
+    }
+    if (tid == 0) s_full = 0;
+  }
+
+  // ---- 2. dense stages in registers; the masked raw logits are kept in LDS
+  const float inv_t = r.do_temp ? r.inv_temp : 1.0f;  // x * 1.0f is exact
+  float x[NE];
+  float lmax = neg_inf();
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const uint32_t off = s * TILE + tid * EPL;  // chunk-local
+    float v[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      v[e] = __uint_as_float(raw[s][e]);
+      if (MASK && !((mw[s] >> ((c0 + off + e) & 31)) & 1u)) v[e] = neg_inf();
+    }
+    if (c0 + off >= c1) {  // past the end of a short last chunk
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) v[e] = neg_inf();
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4) *(float4*)&s_x[off + e] = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float y = v[e] * inv_t;
+      x[s * EPL + e] = y;
+      lmax = fmaxf(lmax, y);  // a NaN here only lowers the pruning, never correctness
+      if (WB && c0 + off + e < c1) p.logits_out[(size_t)row * p.logits_out_ld + c0 + off + e] = y;
+    }
+  }
+
+  // ---- 3. wavefront threshold: a lower bound of the c_w-th largest lane
+  // maximum, from the top 16 bits of the order keys
+  const uint32_t lm = f2ord(lmax);
+  uint32_t theta = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 16; --bit) {
+    const uint32_t trial = theta | (1u << bit);
+    if ((uint32_t)__popcll(__ballot(lm >= trial)) >= p.c_w) theta = trial;
+  }
+  float theta_f;
+  if (theta < kMinValidOrd) {  // too few candidates: keep every one
+    theta = kMinValidOrd;
+    theta_f = -__FLT_MAX__;
+  } else {
+    theta_f = ord2f(theta);
+  }
+  uint32_t smask = 0;  // bit i: x[i] >= theta_f (false for -inf and NaN)
+#pragma unroll
+  for (int i = 0; i < NE; ++i) smask |= (x[i] >= theta_f ? 1u : 0u) << i;
+
+  // ---- 4. mark the chunk's sparse-stage ids (bans, biases, newline, history)
+  if (r.any_special) {
+    __syncthreads();  // LDS tables cleared
+    bool ok = true;
+#pragma unroll
+    for (int q = 0; q < kHistUnroll; ++q) {
+      const uint32_t t = hv[q];
+      if (t >= c0 && t < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, t - c0, 1u, 0u);
+    }
+    if (r.use_hist) {
+      for (uint32_t j = tid + kHistUnroll * kThreads; j < r.wn; j += kThreads) {  // long windows
+        const uint32_t t = hrow[j];
+        if (t >= c0 && t < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, t - c0, 1u, 0u);
+      }
+    }
+    for (uint32_t k = tid; k < r.ban_cnt; k += kThreads) {
+      const uint32_t id = p.ban_ids[r.ban_off + k];
+      if (id >= c0 && id < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBanFlag);
+    }
+    for (uint32_t k = tid; k < r.bias_cnt; k += kThreads) {
+      const uint32_t id = p.bias_ids[r.bias_off + k];
+      if (id >= c0 && id < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBiasFlag);
+    }
+    if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1)
+      ok &= mark(s_bitmap, s_hkeys, s_hvals, r.nl_id - c0, 0u, kNlFlag);
+    if (!ok) s_full = 1;
+    __syncthreads();  // marks complete
+  }
+
+  // ---- 5. survivors (unmarked, x >= theta_f) into this wavefront's list
+  const size_t wslot = ((size_t)row * p.S + chunk) * kWavesPerBlock + wave;
+  uint64_t* out = p.lists + wslot * p.cap_w;
+  while (smask) {
+    const uint32_t b = __builtin_ctz(smask);
+    smask &= smask - 1u;
+    const uint32_t off = (b / EPL) * TILE + tid * EPL + (b % EPL);
+    if (r.any_special && ((s_bitmap[off >> 5] >> (off & 31)) & 1u)) continue;
+    const float y = s_x[off] * inv_t;
+    const uint32_t q = atomicAdd(&s_wcount[wave], 1u);
+    if (q < p.cap_w) out[q] = comp_key(f2ord(y), c0 + off);
+    else s_wover[wave] = 1u;
+  }
+  if (lane == 0) s_wtheta[wave] = theta;
+
+  // ---- 6. exact values of the marked ids; those at or above the block's
+  // largest threshold join the lists (the tail drops smaller keys)
+  if (r.any_special) {
+    __syncthreads();
+    uint32_t tb = s_wtheta[0];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) tb = max(tb, s_wtheta[w]);
+    for (uint32_t h = tid; h < (uint32_t)kHashSlots; h += kThreads) {
+      const uint32_t off = s_hkeys[h];
+      if (off == kEmpty) continue;
+      const uint32_t idx = c0 + off;
+      float y = apply_special(p.bias_ids, p.bias_values, r, s_x[off], s_hvals[h], idx);
+      y *= inv_t;
+      if (WB) p.logits_out[(size_t)row * p.logits_out_ld + idx] = y;
+      const uint32_t k = cand_key(y);
+      if (k && k >= tb) {
+        const uint32_t q = atomicAdd(&s_wcount[wave], 1u);
+        if (q < p.cap_w) out[q] = comp_key(k, idx);
+        else s_wover[wave] = 1u;
+      }
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+    const bool bad = s_wover[wave] != 0u || (r.any_special && s_full != 0u);
+    p.wave_theta[wslot] = bad ? ~0ull : ((uint64_t)theta << 32);
+    p.wave_count[wslot] = bad ? 0u : min(s_wcount[wave], p.cap_w);
+  }
+}
+
+// ---------------------------------------------------------------- tail helpers
 
 struct TailShared {
-  uint32_t hist[256];
-  uint32_t woff[kMaxChunks * kWavesPerBlock];
   uint32_t wcnt[kMaxChunks * kWavesPerBlock];
   uint32_t scan_scratch[8];
   uint64_t red_scratch[8];
   uint32_t sel_digit, sel_above, sel_count, counter;
-  uint32_t n, status, token;
-  float inv;
+  uint32_t n, token, first;
+  float f;
 };
-
-// Radix-select step: given a histogram of the next digit among keys matching
-// the current prefix, finds the digit holding the kk-th largest key.
-__device__ void find_digit(TailShared& ts, uint32_t kk) {
-  const uint32_t t = threadIdx.x;
-  const uint32_t d = 255u - t;
-  uint32_t h = ts.hist[d];
-  uint32_t tot;
-  uint32_t above = block_excl_scan(h, &tot, ts.scan_scratch);
-  if (above < kk && kk <= above + h) {
-    ts.sel_digit = d;
-    ts.sel_above = above;
-    ts.sel_count = h;
-  }
-  __syncthreads();
-}
-
-// The k-th largest of n distinct keys in LDS (1 <= k <= n).
-__device__ uint64_t kth_largest(const uint64_t* keys, uint32_t n, uint32_t k, TailShared& ts) {
-  const uint32_t tid = threadIdx.x;
-  uint64_t prefix = 0, mask = 0;
-  uint32_t kk = k;
-  for (int d = 0; d < 8; ++d) {
-    const int shift = 56 - 8 * d;
-    ts.hist[tid] = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < n; i += kThreads) {
-      uint64_t key = keys[i];
-      if ((key & mask) == prefix) atomicAdd(&ts.hist[(uint32_t)(key >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    find_digit(ts, kk);
-    prefix |= (uint64_t)ts.sel_digit << shift;
-    mask |= 0xffull << shift;
-    kk -= ts.sel_above;
-    const uint32_t cnt = ts.sel_count;
-    __syncthreads();
-    if (cnt == kk) {  // every key of this bucket is in: the k-th is the bucket minimum
-      uint64_t mn = ~0ull;
-      for (uint32_t i = tid; i < n; i += kThreads) {
-        uint64_t key = keys[i];
-        if ((key & mask) == prefix && key < mn) mn = key;
-      }
-      return block_min_u64(mn, ts.red_scratch);
-    }
-  }
-  return prefix;
-}
 
 // Sorts n keys in LDS descending (ascending if ASC), padding to a power of two.
 template <bool ASC>
@@ -368,11 +536,11 @@ __device__ void bitonic_sort(uint64_t* a, uint32_t n) {
   for (uint32_t k = 2; k <= n2; k <<= 1) {
     for (uint32_t j = k >> 1; j > 0; j >>= 1) {
       for (uint32_t i = tid; i < n2; i += kThreads) {
-        uint32_t ixj = i ^ j;
+        const uint32_t ixj = i ^ j;
         if (ixj > i) {
-          uint64_t x = a[i], y = a[ixj];
-          bool second_half = (i & k) != 0;
-          bool swap = ASC ? (second_half ? (x < y) : (x > y)) : (second_half ? (x > y) : (x < y));
+          const uint64_t x = a[i], y = a[ixj];
+          const bool second_half = (i & k) != 0;
+          const bool swap = ASC ? (second_half ? (x < y) : (x > y)) : (second_half ? (x > y) : (x < y));
           if (swap) {
             a[i] = y;
             a[ixj] = x;
@@ -384,48 +552,104 @@ __device__ void bitonic_sort(uint64_t* a, uint32_t n) {
   }
 }
 
-// Exact top-M of a whole row without the phase-A candidate sets: a radix
-// select over all V keys, re-reading the row once per digit. Used only when
-// the candidate union cannot be proven to hold the row's top M. Writes the
-// top min(M, pool) keys to out (unordered); returns that count.
+// Radix-select step: given a histogram of the next digit among keys matching
+// the current prefix, finds the digit holding the kk-th largest key.
+__device__ void find_digit(const uint32_t* hist, TailShared& ts, uint32_t kk) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t d = 255u - t;
+  const uint32_t h = hist[d];
+  uint32_t tot;
+  const uint32_t above = block_excl_scan(h, &tot, ts.scan_scratch);
+  if (above < kk && kk <= above + h) {
+    ts.sel_digit = d;
+    ts.sel_above = above;
+    ts.sel_count = h;
+  }
+  __syncthreads();
+}
+
+// Dense penalty table of logits [c0, c1) for the exact path: window counts in
+// the low bits, ban/bias/newline flags in the high bits. Ends with a barrier.
+__device__ void build_table(const Params& p, const RowXf& r, uint32_t row, uint32_t c0,
+                            uint32_t c1, uint32_t* table) {
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t i = tid; i < c1 - c0; i += kThreads) table[i] = 0;
+  __syncthreads();
+  if (r.use_hist) {
+    const uint32_t* h = p.history + (size_t)row * p.history_ld + r.wstart;
+    for (uint32_t j = tid; j < r.wn; j += kThreads) {
+      const uint32_t t = h[j];
+      if (t >= c0 && t < c1) atomicAdd(&table[t - c0], 1u);
+    }
+  }
+  for (uint32_t k = tid; k < r.ban_cnt; k += kThreads) {
+    const uint32_t id = p.ban_ids[r.ban_off + k];
+    if (id >= c0 && id < c1) atomicOr(&table[id - c0], kBanFlag);
+  }
+  for (uint32_t k = tid; k < r.bias_cnt; k += kThreads) {
+    const uint32_t id = p.bias_ids[r.bias_off + k];
+    if (id >= c0 && id < c1) atomicOr(&table[id - c0], kBiasFlag);
+  }
+  if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1) atomicOr(&table[r.nl_id - c0], kNlFlag);
+  __syncthreads();
+}
+
+template <int DT>
+__device__ __forceinline__ float transformed_logit(const Params& p, const RowXf& r, uint32_t row,
+                                                   uint32_t idx, uint32_t c0,
+                                                   const uint32_t* table) {
+  float x = load_logit<DT>(p, row, idx);
+  if (p.mask && !mask_allows(p, row, idx)) x = neg_inf();
+  if (r.any_special) {
+    const uint32_t e = table[idx - c0];
+    if (e) x = apply_special(p.bias_ids, p.bias_values, r, x, e, idx);
+  }
+  if (r.do_temp) x *= r.inv_temp;
+  return x;
+}
+
+// Exact top-M of a whole row without the candidate sets: a radix select over
+// all V keys, re-reading the row once per digit. Used only when the candidate
+// keys cannot be proven to hold the row's top M. Writes the top min(M, pool)
+// keys to out (unordered); returns that count.
 template <int DT>
 __device__ uint32_t exact_select_row(const Params& p, const RowXf& r, uint32_t row, uint32_t M,
-                                     uint32_t* table, uint64_t* out, TailShared& ts) {
+                                     uint32_t* table, uint32_t* hist, uint64_t* out,
+                                     TailShared& ts) {
   const uint32_t tid = threadIdx.x;
   uint64_t prefix = 0, mask = 0;
   uint32_t kk = 0, meff = 0;
   bool done = false;
   for (int d = 0; d < 8 && !done; ++d) {
     const int shift = 56 - 8 * d;
-    ts.hist[tid] = 0;
+    hist[tid] = 0;
     __syncthreads();
     for (uint32_t c = 0; c < p.S; ++c) {
       const uint32_t c0 = c * p.CH;
       const uint32_t c1 = min(c0 + p.CH, p.V);
       if (r.any_special) build_table(p, r, row, c0, c1, table);
       for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
-        uint32_t k = cand_key(transformed_logit<DT>(p, r, row, i, c0, table));
+        const uint32_t k = cand_key(transformed_logit<DT>(p, r, row, i, c0, table));
         if (!k) continue;
-        uint64_t key = comp_key(k, i);
-        if ((key & mask) == prefix) atomicAdd(&ts.hist[(uint32_t)(key >> shift) & 255u], 1u);
+        const uint64_t key = comp_key(k, i);
+        if ((key & mask) == prefix) atomicAdd(&hist[(uint32_t)(key >> shift) & 255u], 1u);
       }
       __syncthreads();
     }
     if (d == 0) {
       uint32_t pool;
-      block_excl_scan(ts.hist[tid], &pool, ts.scan_scratch);
+      block_excl_scan(hist[tid], &pool, ts.scan_scratch);
       meff = min(M, pool);
       kk = meff;
       if (meff == 0) return 0;
     }
-    find_digit(ts, kk);
+    find_digit(hist, ts, kk);
     prefix |= (uint64_t)ts.sel_digit << shift;
     mask |= 0xffull << shift;
     kk -= ts.sel_above;
     if (ts.sel_count == kk) done = true;  // the whole bucket is in
     __syncthreads();
   }
-  // Collect every key whose leading digits reach the selected bucket.
   if (tid == 0) ts.counter = 0;
   __syncthreads();
   for (uint32_t c = 0; c < p.S; ++c) {
@@ -433,17 +657,97 @@ __device__ uint32_t exact_select_row(const Params& p, const RowXf& r, uint32_t r
     const uint32_t c1 = min(c0 + p.CH, p.V);
     if (r.any_special) build_table(p, r, row, c0, c1, table);
     for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
-      uint32_t k = cand_key(transformed_logit<DT>(p, r, row, i, c0, table));
+      const uint32_t k = cand_key(transformed_logit<DT>(p, r, row, i, c0, table));
       if (!k) continue;
-      uint64_t key = comp_key(k, i);
+      const uint64_t key = comp_key(k, i);
       if ((key & mask) >= prefix) {
-        uint32_t pos = atomicAdd(&ts.counter, 1u);
+        const uint32_t pos = atomicAdd(&ts.counter, 1u);
         if (pos < (uint32_t)kMaxM) out[pos] = key;
       }
     }
     __syncthreads();
   }
   return meff;
+}
+
+__device__ __forceinline__ float key_value(uint64_t k) { return ord2f((uint32_t)(k >> 32)); }
+
+// The M largest of n distinct keys u[0..n), sorted descending, into out[0..M).
+// Counting sort over kBuckets buckets that are linear in the float value
+// between the smallest and largest key (rounded subtraction and scaling are
+// monotone, so bucket order agrees with key order), then the exact order
+// inside each bucket by rank. Falls back to a bitonic sort of all n keys when
+// the values are not finite or one needed bucket holds many keys.
+__device__ void select_sorted(uint64_t* u, uint32_t n, uint32_t M, uint64_t* out, uint64_t* tmp,
+                              uint32_t* bstart, uint32_t* bfill, TailShared& ts) {
+  const uint32_t tid = threadIdx.x;
+  uint64_t kmx = 0, kmn = ~0ull;
+  for (uint32_t i = tid; i < n; i += kThreads) {
+    const uint64_t k = u[i];
+    kmx = k > kmx ? k : kmx;
+    kmn = k < kmn ? k : kmn;
+  }
+  const float vmax = key_value(block_reduce_u64<true>(kmx, ts.red_scratch));
+  const float vmin = key_value(block_reduce_u64<false>(kmn, ts.red_scratch));
+  const float range = vmax - vmin;
+  const float scale = (float)(kBuckets - 1) / range;
+  const bool linear = range > 0.0f && range <= __FLT_MAX__ && scale <= __FLT_MAX__ &&
+                      vmax <= __FLT_MAX__ && vmin >= -__FLT_MAX__;
+  bool fallback = !linear;
+  uint32_t span = 0;
+  if (linear) {
+    for (uint32_t b = tid; b < (uint32_t)kBuckets; b += kThreads) bfill[b] = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < n; i += kThreads) {
+      const uint32_t b = min((uint32_t)((vmax - key_value(u[i])) * scale), (uint32_t)kBuckets - 1);
+      atomicAdd(&bfill[b], 1u);
+    }
+    __syncthreads();
+    static_assert(kBuckets == 4 * kThreads, "4 buckets per thread");
+    uint32_t c4[4], loc = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c4[q] = bfill[tid * 4 + q];
+      loc += c4[q];
+    }
+    uint32_t total;
+    uint32_t run = block_excl_scan(loc, &total, ts.scan_scratch);
+    uint32_t mxb = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bstart[tid * 4 + q] = run;
+      if (run < M) mxb = c4[q] > mxb ? c4[q] : mxb;  // largest needed bucket
+      if (run < M && run + c4[q] >= M) ts.sel_digit = tid * 4 + q;  // bucket of the M-th key
+      run += c4[q];
+    }
+    const uint32_t big = (uint32_t)block_reduce_u64<true>(mxb, ts.red_scratch);
+    const uint32_t last = ts.sel_digit;
+    span = last + 1 < (uint32_t)kBuckets ? bstart[last + 1] : total;  // keys in buckets <= last
+    fallback = big > 64 || span > 2u * kMaxM;
+    if (!fallback) {
+      for (uint32_t b = tid; b < (uint32_t)kBuckets; b += kThreads) bfill[b] = bstart[b];
+      __syncthreads();
+      for (uint32_t i = tid; i < n; i += kThreads) {
+        const uint64_t k = u[i];
+        const uint32_t b = min((uint32_t)((vmax - key_value(k)) * scale), (uint32_t)kBuckets - 1);
+        if (b <= last) tmp[atomicAdd(&bfill[b], 1u)] = k;
+      }
+      __syncthreads();
+      for (uint32_t i = tid; i < span; i += kThreads) {
+        const uint64_t k = tmp[i];
+        const uint32_t b = min((uint32_t)((vmax - key_value(k)) * scale), (uint32_t)kBuckets - 1);
+        const uint32_t lo = bstart[b], hi = bfill[b];
+        uint32_t rank = lo;
+        for (uint32_t j = lo; j < hi; ++j) rank += tmp[j] > k ? 1u : 0u;
+        if (rank < M) out[rank] = k;
+      }
+      __syncthreads();
+      return;
+    }
+  }
+  bitonic_sort<false>(u, n);
+  for (uint32_t i = tid; i < M; i += kThreads) out[i] = u[i];
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- tail math
@@ -461,230 +765,280 @@ __device__ __forceinline__ float next_f32(uint64_t* s) {  // sampler.rs:139-153
   x ^= x >> 7;
   x ^= x << 17;
   *s = x;
-  uint32_t val = (uint32_t)(x >> 40);
+  const uint32_t val = (uint32_t)(x >> 40);
   return (float)val / 16777216.0f;
 }
 
-// The post-top-M chain of sampler.rs:286-389 for one row. keys[0..n) are
-// sorted descending. LDS scratch: ids/pr/aux each kMaxM entries.
+// The reference's ordered f32 running sums, computed by one thread from
+// registers: 64 values at a time are read with 16-byte LDS loads, then added
+// in index order. Adds f(a[i]) for i = 0, 1, ... to `init` and stops after the
+// first i whose running sum reaches `stop` (when USE_STOP) or at n; returns
+// that index + 1 (n when it never stops) and the running sum. `a` must be
+// 16-byte aligned and readable up to the next multiple of 64 entries.
+struct Chain {
+  uint32_t stop;
+  float sum;
+};
+
+template <bool USE_STOP, typename F>
+__device__ __noinline__ Chain lane_chain(const float* a, uint32_t n, float init, float stop, F f) {
+  float s = init;
+  for (uint32_t base = 0; base < n; base += 64) {
+    float v[64];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float4 t = *(const float4*)(a + base + 4 * q);
+      v[4 * q] = t.x;
+      v[4 * q + 1] = t.y;
+      v[4 * q + 2] = t.z;
+      v[4 * q + 3] = t.w;
+    }
+    if (base + 64 <= n) {
+#pragma unroll
+      for (int j = 0; j < 64; ++j) {
+        s += f(v[j]);
+        if (USE_STOP && s >= stop) return Chain{base + j + 1, s};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 64; ++j) {
+        if (base + j < n) {
+          s += f(v[j]);
+          if (USE_STOP && s >= stop) return Chain{base + j + 1, s};
+        }
+      }
+    }
+  }
+  return Chain{n, s};
+}
+
+struct Ident {
+  __device__ float operator()(float v) const { return v; }
+};
+struct Scaled {
+  float k;
+  __device__ float operator()(float v) const { return v * k; }
+};
+
+// Stable block-wide compaction of (ids, pr)[0..n) keeping keep(i); returns the count.
+template <typename F>
+__device__ uint32_t compact_stable(uint32_t* ids, float* pr, uint32_t* ids2, float* pr2, uint32_t n,
+                                   F keep, TailShared& ts) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t base = 0;
+  for (uint32_t r0 = 0; r0 < n; r0 += kThreads) {
+    const uint32_t i = r0 + tid;
+    const bool k = i < n && keep(i);
+    uint32_t tot;
+    const uint32_t pos = base + block_excl_scan(k ? 1u : 0u, &tot, ts.scan_scratch);
+    if (k) {
+      ids2[pos] = ids[i];
+      pr2[pos] = pr[i];
+    }
+    base += tot;
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < base; i += kThreads) {
+    ids[i] = ids2[i];
+    pr[i] = pr2[i];
+  }
+  __syncthreads();
+  return base;
+}
+
+__device__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status) {
+  if (threadIdx.x == 0) {
+    p.out_tokens[row] = token;
+    if (p.out_status) p.out_status[row] = status;
+    if (p.out_kept_count) p.out_kept_count[row] = 0;
+  }
+}
+
+// Moves (ids, pr)[from .. from+len) to [0, len) through the spare arrays.
+__device__ void shift_down(uint32_t* ids, float* pr, uint32_t* ids2, float* pr2, uint32_t from,
+                           uint32_t len) {
+  for (uint32_t i = threadIdx.x; i < len; i += kThreads) {
+    ids2[i] = ids[from + i];
+    pr2[i] = pr[from + i];
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < len; i += kThreads) {
+    ids[i] = ids2[i];
+    pr[i] = pr2[i];
+  }
+  __syncthreads();
+}
+
+// The chain after the top-M selection (sampler.rs:286-389) on keys[0..n),
+// sorted descending. ids/pr/ids2/pr2 hold kMaxM entries each (contiguous, in
+// that order); aux holds 2 * kMaxM keys. Parallel stages use the whole block;
+// the reference's ordered f32 sums run in thread 0 (lane_chain).
 __device__ void tail_chain(const Params& p, const oxs_sampling_config& c, uint32_t row,
-                           uint64_t* keys, uint32_t n, uint32_t* ids, float* pr, uint64_t* aux,
-                           TailShared& ts) {
+                           const uint64_t* keys, uint32_t n, uint32_t* ids, float* pr,
+                           uint32_t* ids2, float* pr2, uint64_t* aux, TailShared& ts) {
   const uint32_t tid = threadIdx.x;
   // Softmax over the n kept candidates (:286-295).
+  const float max_logit = key_value(keys[0]);
   for (uint32_t i = tid; i < n; i += kThreads) {
-    uint64_t k = keys[i];
+    const uint64_t k = keys[i];
     ids[i] = ~(uint32_t)k;
-    pr[i] = ord2f((uint32_t)(k >> 32));
+    pr[i] = dexpf(key_value(k) - max_logit);
   }
-  __syncthreads();
-  const float max_logit = pr[0];
-  __syncthreads();
-  for (uint32_t i = tid; i < n; i += kThreads) pr[i] = dexpf(pr[i] - max_logit);
   __syncthreads();
   if (tid == 0) {
-    float sum_exp = 0.0f;
-    for (uint32_t i = 0; i < n; ++i) sum_exp += pr[i];
-    ts.inv = sum_exp > 0.0f ? 1.0f / sum_exp : 1.0f;
+    const float sum_exp = lane_chain<false>(pr, n, 0.0f, 0.0f, Ident{}).sum;
+    ts.f = sum_exp > 0.0f ? 1.0f / sum_exp : 1.0f;
   }
   __syncthreads();
-  const float inv_sum = ts.inv;
+  const float inv_sum = ts.f;
   for (uint32_t i = tid; i < n; i += kThreads) pr[i] *= inv_sum;
   __syncthreads();
 
-  const bool record = (p.flags & OXS_FLAG_RECORD_HISTORY) != 0;
-  uint32_t len = n;  // current candidate count (list lives in ids/pr[0..len))
-  uint32_t token = 0;
-  uint32_t n_record = 1;
-
+  uint32_t len = n, n_record = 1;
   if (c.mirostat_mode == OXS_MIROSTAT_V1 || c.mirostat_mode == OXS_MIROSTAT_V2) {
+    const float mu0 = p.mu[row];
+    if (c.mirostat_mode == OXS_MIROSTAT_V2) {  // :432-456
+      // the included prefix ends before the first i > 0 whose surprise exceeds mu
+      if (tid == 0) ts.first = n;
+      __syncthreads();
+      for (uint32_t i = tid; i < n; i += kThreads) {
+        const float surprise = -dlog2f(fmaxf(pr[i], 1e-8f));
+        if (i > 0 && surprise > mu0) atomicMin(&ts.first, i);
+      }
+      __syncthreads();
+    }
     if (tid == 0) {
-      float mu = p.mu[row];
+      float mu = mu0;
       if (c.mirostat_mode == OXS_MIROSTAT_V1) {  // :418-429
-        float prob = fmaxf(pr[0], 1e-6f);
-        float surprise = -dlog2f(prob);
-        float error = surprise - c.mirostat_tau;
-        float step = c.mirostat_eta * error;
+        const float prob = fmaxf(pr[0], 1e-6f);
+        const float surprise = -dlog2f(prob);
+        const float error = surprise - c.mirostat_tau;
+        const float step = c.mirostat_eta * error;
         mu -= step;
-      } else {  // :432-456
-        float max_surprise = mu;
-        float cum_prob = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) {
-          float surprise = -dlog2f(fmaxf(pr[i], 1e-8f));
-          if (surprise > max_surprise && i > 0) break;
-          cum_prob += pr[i];
-        }
-        float prob = pr[0] / fmaxf(cum_prob, 1e-6f);
-        float surprise = -dlog2f(fmaxf(prob, 1e-8f));
-        float error = surprise - c.mirostat_tau;
-        float step = c.mirostat_eta * error;
+      } else {
+        const float cum_prob = lane_chain<false>(pr, ts.first, 0.0f, 0.0f, Ident{}).sum;
+        const float prob = pr[0] / fmaxf(cum_prob, 1e-6f);
+        const float surprise = -dlog2f(fmaxf(prob, 1e-8f));
+        const float error = surprise - c.mirostat_tau;
+        const float step = c.mirostat_eta * error;
         mu -= step;
       }
       p.mu[row] = mu;
       ts.token = ids[0];
-      ts.n = n;
     }
     n_record = 2;  // recorded inside the mode function and by the caller (:301, :307)
   } else {
-    if (tid == 0) {
-      uint32_t start = 0;
-      // Min-p (:315-319): keep p >= p_max * min_p, in order.
-      if (c.min_p > 0.0f && len > 0) {
-        float threshold = pr[0] * c.min_p;
-        uint32_t w = 0;
-        for (uint32_t i = 0; i < len; ++i) {
-          if (pr[i] >= threshold) {
-            pr[w] = pr[i];
-            ids[w] = ids[i];
-            ++w;
-          }
-        }
-        len = w;
-      }
-      // XTC (:322-328).
-      if (c.xtc_probability > 0.0f && len > 1) {
-        float p_max = pr[0];
-        if (p_max >= c.xtc_threshold && p_max < 0.98f) start = 1;
-      }
-      uint32_t cnt = len - start;
-      // Top-k (:331-333).
-      if (c.top_k > 0 && cnt > c.top_k) cnt = c.top_k;
-      // Tail-free (:336-338, :459-490).
-      if (c.tfs_z < 1.0f && cnt > 2) {
-        const float* q = pr + start;
-        float sum_d2 = 0.0f;
-        for (uint32_t i = 0; i + 2 < cnt; ++i) {
-          float d1a = q[i] - q[i + 1];
-          float d1b = q[i + 1] - q[i + 2];
-          sum_d2 += fabsf(d1a - d1b);
-        }
-        if (sum_d2 > 0.0f) {
-          float inv = 1.0f / sum_d2;
-          float cum = 0.0f;
-          uint32_t cutoff = cnt;
-          for (uint32_t i = 0; i + 2 < cnt; ++i) {
-            float d1a = q[i] - q[i + 1];
-            float d1b = q[i + 1] - q[i + 2];
-            float t = fabsf(d1a - d1b) * inv;
-            cum += t;
-            if (cum >= c.tfs_z) {
-              cutoff = i + 1;
-              break;
-            }
-          }
-          cnt = cutoff > 1 ? cutoff : 1;
-        }
-      }
-      // Compact to [0, cnt) for the stages that follow.
-      if (start) {
-        for (uint32_t i = 0; i < cnt; ++i) {
-          pr[i] = pr[i + start];
-          ids[i] = ids[i + start];
-        }
-      }
-      ts.n = cnt;
+    // Min-p (:315-319): keep p >= p_max * min_p, in order.
+    if (c.min_p > 0.0f && len > 0) {
+      const float threshold = pr[0] * c.min_p;
+      len = compact_stable(ids, pr, ids2, pr2, len, [=](uint32_t i) { return pr[i] >= threshold; }, ts);
     }
-    __syncthreads();
-    len = ts.n;
-    // Locally typical (:341-343, :493-520): stable sort by |surprisal - H|.
-    if (c.typical_p < 1.0f && len > 1) {
-      if (tid == 0) {
-        float entropy = -0.0f;
-        for (uint32_t i = 0; i < len; ++i) {
-          float term = pr[i] > 0.0f ? (-pr[i]) * dlogf(pr[i]) : 0.0f;
-          entropy += term;
-        }
-        ts.inv = entropy;
+    // XTC (:322-328): drop the top choice.
+    if (c.xtc_probability > 0.0f && len > 1) {
+      const float p_max = pr[0];
+      if (p_max >= c.xtc_threshold && p_max < 0.98f) {
+        shift_down(ids, pr, ids2, pr2, 1, len - 1);
+        len -= 1;
       }
-      __syncthreads();
-      const float entropy = ts.inv;
-      for (uint32_t i = tid; i < len; i += kThreads) {
-        float surprisal = pr[i] > 0.0f ? -dlogf(pr[i]) : 0.0f;
-        float diff = fabsf(surprisal - entropy);
-        aux[i] = ((uint64_t)f2ord(diff) << 32) | i;  // ascending score, then position
-      }
-      __syncthreads();
-      bitonic_sort<true>(aux, len);
-      // Gather into keys[] as (id, p) pairs, then back.
-      for (uint32_t i = tid; i < len; i += kThreads) {
-        uint32_t src = (uint32_t)aux[i];
-        keys[i] = ((uint64_t)ids[src] << 32) | __float_as_uint(pr[src]);
-      }
-      __syncthreads();
-      for (uint32_t i = tid; i < len; i += kThreads) {
-        ids[i] = (uint32_t)(keys[i] >> 32);
-        pr[i] = __uint_as_float((uint32_t)keys[i]);
+    }
+    // Top-k (:331-333).
+    if (c.top_k > 0 && len > c.top_k) len = c.top_k;
+    // Tail-free (:336-338, :459-490).
+    if (c.tfs_z < 1.0f && len > 2) {
+      float* d2 = pr2;
+      const uint32_t m = len - 2;
+      for (uint32_t i = tid; i < m; i += kThreads) {
+        const float d1a = pr[i] - pr[i + 1];
+        const float d1b = pr[i + 1] - pr[i + 2];
+        d2[i] = fabsf(d1a - d1b);
       }
       __syncthreads();
       if (tid == 0) {
-        float cum = 0.0f;
+        const float sum_d2 = lane_chain<false>(d2, m, 0.0f, 0.0f, Ident{}).sum;
         uint32_t keep = len;
-        for (uint32_t i = 0; i < len; ++i) {
-          cum += pr[i];
-          if (cum >= c.typical_p) {
-            keep = i + 1;
-            break;
-          }
+        if (sum_d2 > 0.0f) {
+          const float inv = 1.0f / sum_d2;
+          const Chain ch = lane_chain<true>(d2, m, 0.0f, c.tfs_z, Scaled{inv});
+          const uint32_t cutoff = ch.stop < m || ch.sum >= c.tfs_z ? ch.stop : len;
+          keep = cutoff > 1 ? cutoff : 1;
         }
         ts.n = keep;
       }
       __syncthreads();
       len = ts.n;
     }
-    if (tid == 0) {
-      // Top-p (:346-357).
-      if (c.top_p < 1.0f) {
-        float cumulative = 0.0f;
-        uint32_t cut = len;
-        for (uint32_t i = 0; i < len; ++i) {
-          cumulative += pr[i];
-          if (cumulative >= c.top_p) {
-            cut = i + 1;
-            break;
-          }
-        }
-        len = cut;
+    // Locally typical (:341-343, :493-520): stable sort by |surprisal - H|.
+    if (c.typical_p < 1.0f && len > 1) {
+      float* terms = pr2;
+      for (uint32_t i = tid; i < len; i += kThreads) terms[i] = pr[i] > 0.0f ? (-pr[i]) * dlogf(pr[i]) : 0.0f;
+      __syncthreads();
+      if (tid == 0) ts.f = lane_chain<false>(terms, len, -0.0f, 0.0f, Ident{}).sum;
+      __syncthreads();
+      const float entropy = ts.f;
+      for (uint32_t i = tid; i < len; i += kThreads) {
+        const float surprisal = pr[i] > 0.0f ? -dlogf(pr[i]) : 0.0f;
+        const float diff = fabsf(surprisal - entropy);
+        aux[i] = ((uint64_t)f2ord(diff) << 32) | i;  // ascending score, then position
       }
+      __syncthreads();
+      bitonic_sort<true>(aux, len);
+      for (uint32_t i = tid; i < len; i += kThreads) {
+        const uint32_t src = (uint32_t)aux[i];
+        ids2[i] = ids[src];
+        pr2[i] = pr[src];
+      }
+      __syncthreads();
+      for (uint32_t i = tid; i < len; i += kThreads) {
+        ids[i] = ids2[i];
+        pr[i] = pr2[i];
+      }
+      __syncthreads();
+      if (tid == 0) ts.n = lane_chain<true>(pr, len, 0.0f, c.typical_p, Ident{}).stop;
+      __syncthreads();
+      len = ts.n;
+    }
+    if (tid == 0) {
+      // Top-p (:346-357): cut at the first running sum >= top_p.
+      uint32_t cut = len;
+      if (c.top_p < 1.0f) cut = lane_chain<true>(pr, len, 0.0f, c.top_p, Ident{}).stop;
       // Renormalise (:360-368).
-      float total = -0.0f;
-      for (uint32_t i = 0; i < len; ++i) total += pr[i];
-      float inv_total = total > 0.0f ? 1.0f / total : 1.0f;
-      for (uint32_t i = 0; i < len; ++i) pr[i] *= inv_total;
-      // Draw (:371-385).
+      const float total = lane_chain<false>(pr, cut, -0.0f, 0.0f, Ident{}).sum;
+      ts.f = total > 0.0f ? 1.0f / total : 1.0f;
+      ts.n = cut;
+    }
+    __syncthreads();
+    len = ts.n;
+    const float inv_total = ts.f;
+    for (uint32_t i = tid; i < len; i += kThreads) pr[i] *= inv_total;
+    __syncthreads();
+    if (tid == 0) {
+      // Draw (:371-385): greedy below 1e-6, else the first running sum >= r;
+      // the fallback is the first candidate.
       uint32_t picked;
       if (c.temperature <= 1e-6f) {
         picked = len ? ids[0] : 0u;
       } else {
-        float r;
+        float rnd;
         if (p.uniforms) {
-          r = p.uniforms[row];
+          rnd = p.uniforms[row];
         } else {
-          uint64_t s = p.rng_state[row];
-          r = next_f32(&s);
-          p.rng_state[row] = s;
+          uint64_t st = p.rng_state[row];
+          rnd = next_f32(&st);
+          p.rng_state[row] = st;
         }
-        float acc = 0.0f;
-        uint32_t selected = len ? ids[0] : 0u;
-        for (uint32_t i = 0; i < len; ++i) {
-          acc += pr[i];
-          if (r <= acc) {
-            selected = ids[i];
-            break;
-          }
-        }
-        picked = selected;
+        const Chain ch = lane_chain<true>(pr, len, 0.0f, rnd, Ident{});
+        const bool hit = len > 0 && ch.sum >= rnd && ch.stop >= 1;
+        picked = hit ? ids[ch.stop - 1] : (len ? ids[0] : 0u);
       }
       ts.token = picked;
-      ts.n = len;
     }
   }
   __syncthreads();
-  token = ts.token;
-  len = ts.n;
+  const uint32_t token = ts.token;
   // Outputs: token, status, history, candidates_buffer.
   if (tid == 0) {
     int32_t status = OXS_ROW_OK;
-    if (record) {
+    if (p.flags & OXS_FLAG_RECORD_HISTORY) {
       uint32_t hl = p.history_len[row];
       for (uint32_t k = 0; k < n_record; ++k) {
         if (hl < p.history_cap) {
@@ -707,185 +1061,24 @@ __device__ void tail_chain(const Params& p, const oxs_sampling_config& c, uint32
   }
 }
 
-__device__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status) {
-  if (threadIdx.x == 0) {
-    p.out_tokens[row] = token;
-    if (p.out_status) p.out_status[row] = status;
-    if (p.out_kept_count) p.out_kept_count[row] = 0;
-  }
-}
+// ---------------------------------------------------------------- tail kernel
 
-// ---------------------------------------------------------------- kernel
-
-template <int DT, int SLOTS, bool VEC>
-__global__ __launch_bounds__(kThreads) void sample_kernel(const Params p) {
-  constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;  // logits per 16-byte load
-  constexpr int TILE = kThreads * EPL;
-  constexpr int CH = SLOTS * TILE;
-  constexpr size_t ESZ = (DT == OXS_DTYPE_F32) ? 4 : 2;
-  static_assert(CH <= kMaxChunk, "chunk exceeds the LDS penalty table");
-
-  __shared__ __align__(16) uint64_t smem_a[kUnionMax];  // penalty table, candidate union, tail arrays
-  __shared__ __align__(16) uint64_t smem_keys[kMaxM];   // sorted top-M keys
+template <int DT>
+__global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
+  __shared__ __align__(16) uint64_t smem_u[kUnionMax];  // candidate keys / exact-path table / chain arrays
+  __shared__ __align__(16) uint64_t smem_k[kMaxM];      // sorted top-M keys
+  __shared__ __align__(16) uint64_t smem_t[2 * kMaxM];  // counting-sort scatter / typical-sort keys
+  __shared__ uint32_t s_bstart[kBuckets];
+  __shared__ uint32_t s_bfill[kBuckets];
   __shared__ TailShared ts;
-  __shared__ uint32_t s_last;
 
   const uint32_t tid = threadIdx.x;
-  const uint32_t lane = tid & 63;
-  const uint32_t wave = tid >> 6;
-  // XCD-aware numbering: hardware round-robins workgroups over the 8 XCDs, so
-  // give each XCD a contiguous range of (row, chunk) ids; a row's chunks then
-  // share one L2.
-  const uint32_t vid = (blockIdx.x & 7u) * p.grid_per_xcd + (blockIdx.x >> 3);
-  if (vid >= p.grid_real) return;
-  const uint32_t row = vid / p.S;
-  const uint32_t chunk = vid - row * p.S;
+  const uint32_t row = p.rpx ? grouped_index(blockIdx.x, p.rpx) : blockIdx.x;
+  if (row >= p.B) return;
   const oxs_sampling_config c = p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
   const RowXf r = make_row_xf(p, c, row);
-  uint32_t* table = (uint32_t*)smem_a;
-
-  const uint32_t c0 = chunk * CH;
-  const uint32_t c1 = min(c0 + (uint32_t)CH, p.V);
-  const bool full = (c1 - c0) == (uint32_t)CH;
-
-  // ---- issue every load of this block's chunk
-  uint32_t raw[SLOTS][EPL];
-  uint32_t mw[SLOTS];
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) mw[s] = 0u;
-  const char* rowp = (const char*)p.logits + (size_t)row * (size_t)p.ld * ESZ;
-  if (VEC && full) {
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const uint32_t base = c0 + s * TILE + tid * EPL;
-      const u32x4 q = __builtin_nontemporal_load((const u32x4*)(rowp + (size_t)base * ESZ));
-      if constexpr (DT == OXS_DTYPE_F32) {
-        raw[s][0] = q.x; raw[s][1] = q.y; raw[s][2] = q.z; raw[s][3] = q.w;
-      } else {
-        raw[s][0] = q.x << 16; raw[s][1] = q.x & 0xffff0000u;
-        raw[s][2] = q.y << 16; raw[s][3] = q.y & 0xffff0000u;
-        raw[s][4] = q.z << 16; raw[s][5] = q.z & 0xffff0000u;
-        raw[s][6] = q.w << 16; raw[s][7] = q.w & 0xffff0000u;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const uint32_t idx = c0 + s * TILE + tid * EPL + e;
-        raw[s][e] = idx < c1 ? __float_as_uint(load_logit<DT>(p, row, idx)) : 0xff800000u;
-      }
-    }
-  }
-  if (p.mask) {
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const uint32_t base = c0 + s * TILE + tid * EPL;
-      mw[s] = base < c1 ? p.mask[(size_t)row * p.mask_ld + (base >> 5)] : 0u;
-    }
-  }
-  if (r.any_special) build_table(p, r, row, c0, c1, table);
-
-  // ---- transform in registers, track the lane maximum key
-  uint32_t key[SLOTS][EPL];
-  uint32_t lane_max = 0;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    const uint32_t base = c0 + s * TILE + tid * EPL;
-    uint32_t ent[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) ent[e] = 0;
-    if (r.any_special && base < c1) {
-      if (base + EPL <= c1) {
-#pragma unroll
-        for (int e = 0; e < EPL; e += 4) {
-          uint4 t4 = *(const uint4*)(table + (base - c0) + e);
-          ent[e] = t4.x; ent[e + 1] = t4.y; ent[e + 2] = t4.z; ent[e + 3] = t4.w;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e)
-          if (base + e < c1) ent[e] = table[base - c0 + e];
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const uint32_t idx = base + e;
-      float x = __uint_as_float(raw[s][e]);
-      if (p.mask && !((mw[s] >> (idx & 31)) & 1u)) x = neg_inf();
-      if (ent[e]) x = apply_special(p, r, x, ent[e], idx);
-      if (r.do_temp) x *= r.inv_temp;
-      if (p.logits_out && idx < c1) p.logits_out[(size_t)row * p.logits_out_ld + idx] = x;
-      uint32_t k = (idx < c1) ? cand_key(x) : 0u;
-      key[s][e] = k;
-      lane_max = k > lane_max ? k : lane_max;
-    }
-  }
-
-  // ---- wavefront threshold: the c_w-th largest lane maximum
-  uint32_t theta = 0;
-#pragma unroll 1
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t trial = theta | (1u << bit);
-    if ((uint32_t)__popcll(__ballot(lane_max >= trial)) >= p.c_w) theta = trial;
-  }
-  uint32_t my_cnt = 0;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s)
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) my_cnt += (key[s][e] != 0u && key[s][e] >= theta) ? 1u : 0u;
-  const uint32_t wave_cnt = wave_sum_u32(my_cnt);
-  const uint32_t W = p.S * kWavesPerBlock;
-  const size_t wslot = (size_t)row * W + (size_t)chunk * kWavesPerBlock + wave;
-  uint64_t* out = p.lists + wslot * p.cap_w;
-  uint64_t wtheta;
-  uint32_t emitted;
-  if (wave_cnt <= p.cap_w) {
-    uint32_t pos = 0;
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const uint32_t k = key[s][e];
-        const bool surv = k != 0u && k >= theta;
-        const uint64_t bal = __ballot(surv);
-        if (surv) {
-          const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-          out[pos + below] = comp_key(k, c0 + s * TILE + tid * EPL + e);
-        }
-        pos += (uint32_t)__popcll(bal);
-      }
-    }
-    wtheta = (uint64_t)theta << 32;  // every key >= (theta, any id) was written
-    emitted = wave_cnt;
-  } else {
-    wtheta = ~0ull;  // overflow: prove nothing, force the exact path
-    emitted = 0;
-  }
-  if (lane == 0) {
-    p.wave_theta[wslot] = wtheta;
-    p.wave_count[wslot] = emitted;
-  }
-
-  // ---- last block of the row runs the tail
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    const uint32_t prev = __hip_atomic_fetch_add(&p.tickets[row], 1u, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = prev == p.S - 1;
-    if (last) p.tickets[row] = 0u;  // ready for the next launch
-    s_last = last ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // Rows that ask for stages not run on the device fail loudly.
   const uint32_t M = max(c.top_k, 256u);
-  if (r.dry || M > (uint32_t)kMaxM) {
+  if (r.dry || M > (uint32_t)kMaxM) {  // stages this build does not run on the device
     write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED);
     return;
   }
@@ -894,67 +1087,73 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const Params p) {
     return;
   }
 
-  // 1. wavefront metadata: offsets of each wavefront's keys, largest threshold.
+  // 1. every wavefront's count and threshold, and all key slots at once
+  const uint32_t W = p.S * kWavesPerBlock;
+  const uint32_t span = W * p.cap_w;
   uint32_t wc = 0;
   uint64_t wt = 0;
   if (tid < W) {
     wc = p.wave_count[(size_t)row * W + tid];
     wt = p.wave_theta[(size_t)row * W + tid];
   }
-  uint32_t total;
-  const uint32_t woff = block_excl_scan(wc, &total, ts.scan_scratch);
-  const uint64_t theta_max = block_max_u64(wt, ts.red_scratch);
-  if (tid < W) {
-    ts.woff[tid] = woff;
-    ts.wcnt[tid] = wc;
+  constexpr int kPer = kUnionMax / kThreads;
+  uint64_t lk[kPer];
+  const uint64_t* lrow = p.lists + (size_t)row * span;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const uint32_t i = tid + q * kThreads;
+    lk[q] = i < span ? lrow[i] : 0ull;
   }
-  __syncthreads();
-  // 2. gather the union into LDS
-  uint64_t* U = smem_a;
-  const uint32_t span = W * p.cap_w;
-  for (uint32_t i = tid; i < span; i += kThreads) {
-    const uint32_t w = i / p.cap_w, j = i - w * p.cap_w;
-    if (j < ts.wcnt[w]) U[ts.woff[w] + j] = p.lists[((size_t)row * W + w) * p.cap_w + j];
-  }
+  const uint64_t theta_max = block_reduce_u64<true>(wt, ts.red_scratch);
+  if (tid < W) ts.wcnt[tid] = wc;
   __syncthreads();
 
-  // 3. the exact top min(M, pool)
-  uint32_t meff;
-  bool exact = false;
-  uint64_t km = 1;
-  if (total >= M) {
-    km = kth_largest(U, total, M, ts);
-    meff = M;
-    exact = theta_max > km;
-  } else {
-    meff = total;
-    exact = theta_max != 0;
-  }
-  if (exact) {
-    meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)smem_a, smem_keys, ts);
-  } else {
-    if (tid == 0) ts.counter = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < total; i += kThreads) {
-      const uint64_t k = U[i];
-      if (k >= km) {
-        const uint32_t pos = atomicAdd(&ts.counter, 1u);
-        if (pos < (uint32_t)kMaxM) smem_keys[pos] = k;
-      }
+  // 2. keep the keys at or above the largest threshold
+  uint32_t mine = 0, keepm = 0;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const uint32_t i = tid + q * kThreads;
+    bool k = false;
+    if (i < span) {
+      const uint32_t w = i >> p.cap_shift, j = i & (p.cap_w - 1u);
+      k = j < ts.wcnt[w] && lk[q] >= theta_max && lk[q] != 0ull;
     }
-    __syncthreads();
+    keepm |= (k ? 1u : 0u) << q;
+    mine += k ? 1u : 0u;
   }
-  if (meff == 0) {  // every logit -inf or NaN (:267-270)
-    write_row_result(p, row, 0u, OXS_ROW_EMPTY);
-    return;
+  uint32_t N;
+  uint32_t off = block_excl_scan(mine, &N, ts.scan_scratch);
+  uint64_t* U = smem_u;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q)
+    if ((keepm >> q) & 1u) U[off++] = lk[q];
+  __syncthreads();
+
+  // 3. N >= M keys at or above every wavefront threshold contain the row's
+  // top M; theta_max == kAllValid means every wavefront kept every candidate.
+  uint32_t meff;
+  if (N >= M || theta_max == kAllValid) {
+    meff = min(M, N);
+    if (meff == 0) {  // every logit -inf or NaN (:267-270)
+      write_row_result(p, row, 0u, OXS_ROW_EMPTY);
+      return;
+    }
+    select_sorted(U, N, meff, smem_k, smem_t, s_bstart, s_bfill, ts);
+  } else {
+    meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)smem_u, s_bfill, smem_k, ts);
+    if (meff == 0) {
+      write_row_result(p, row, 0u, OXS_ROW_EMPTY);
+      return;
+    }
+    bitonic_sort<false>(smem_k, meff);
   }
-  bitonic_sort<false>(smem_keys, meff);
 
   // 4. the chain after the top-M selection
-  uint32_t* ids = (uint32_t*)smem_a;
+  uint32_t* ids = (uint32_t*)smem_u;
   float* pr = (float*)(ids + kMaxM);
-  uint64_t* aux = (uint64_t*)(pr + kMaxM);
-  tail_chain(p, c, row, smem_keys, meff, ids, pr, aux, ts);
+  uint32_t* ids2 = (uint32_t*)(pr + kMaxM);
+  float* pr2 = (float*)(ids2 + kMaxM);
+  tail_chain(p, c, row, smem_k, meff, ids, pr, ids2, pr2, smem_t, ts);
 }
 
 // ---------------------------------------------------------------- host side
@@ -971,18 +1170,17 @@ static uint32_t floor_pow2(uint32_t x) {
 }
 
 // Chunking: the largest per-block tile count that still gives >= 1024 blocks
-// (enough to cover 256 CUs several times), capped by the LDS table and by
-// kMaxChunks per row.
+// (several per CU on 256 CUs), within kMaxChunk and kMaxChunks.
 static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
   const uint32_t epl = dtype == OXS_DTYPE_F32 ? 4 : 8;
   const uint32_t tile = kThreads * epl;
   int best = -1;
   const char* env = getenv("OXS_SLOTS");
-  int forced = env ? atoi(env) : 0;
+  const int forced = env ? atoi(env) : 0;
   for (int slots = 8; slots >= 1; slots >>= 1) {
-    uint32_t ch = slots * tile;
+    const uint32_t ch = slots * tile;
     if (ch > (uint32_t)kMaxChunk) continue;
-    uint32_t S = (V + ch - 1) / ch;
+    const uint32_t S = (V + ch - 1) / ch;
     if (S > (uint32_t)kMaxChunks) continue;
     if (forced) {
       if (slots == forced) best = slots;
@@ -997,28 +1195,41 @@ static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
   g->S = (V + g->CH - 1) / g->CH;
   const uint32_t W = g->S * kWavesPerBlock;
   g->cap_w = floor_pow2(min(64u, (uint32_t)kUnionMax / W));
-  uint32_t c = (3u * 256u + W - 1) / W + 6u;
-  g->c_w = max(1u, min(g->cap_w / 2, c));
+  const uint32_t cw = (3u * 256u + W - 1) / W + 6u;
+  g->c_w = max(1u, min(g->cap_w / 2, cw));
   return true;
 }
 
-template <int DT, int SLOTS, bool VEC>
-static hipError_t launch_t(const Params& p, hipStream_t st) {
-  const uint32_t grid = 8u * p.grid_per_xcd;
-  hipLaunchKernelGGL((sample_kernel<DT, SLOTS, VEC>), dim3(grid), dim3(kThreads), 0, st, p);
+template <int DT, int SLOTS, bool VEC, bool MASK>
+static hipError_t launch_stream(const Params& p, uint32_t grid, hipStream_t st) {
+  if (p.logits_out)
+    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, true>), dim3(grid), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, false>), dim3(grid), dim3(kThreads), 0, st, p);
   return hipGetLastError();
 }
 
-template <int DT, bool VEC>
-static hipError_t launch_slots(int slots, const Params& p, hipStream_t st) {
+template <int DT, bool VEC, bool MASK>
+static hipError_t launch_slots(int slots, const Params& p, uint32_t grid, hipStream_t st) {
   switch (slots) {
     case 8:
-      if constexpr (DT == OXS_DTYPE_F32) return launch_t<DT, 8, VEC>(p, st);
+      if constexpr (DT == OXS_DTYPE_F32) return launch_stream<DT, 8, VEC, MASK>(p, grid, st);
       return hipErrorInvalidValue;  // bf16 chunks stop at 4 slots (8192 logits)
-    case 4: return launch_t<DT, 4, VEC>(p, st);
-    case 2: return launch_t<DT, 2, VEC>(p, st);
-    default: return launch_t<DT, 1, VEC>(p, st);
+    case 4: return launch_stream<DT, 4, VEC, MASK>(p, grid, st);
+    case 2: return launch_stream<DT, 2, VEC, MASK>(p, grid, st);
+    default: return launch_stream<DT, 1, VEC, MASK>(p, grid, st);
   }
+}
+
+template <int DT>
+static hipError_t launch_all(int slots, bool vec, bool mask, const Params& p, uint32_t grid_a,
+                             uint32_t grid_b, hipStream_t st) {
+  hipError_t e;
+  if (vec) e = mask ? launch_slots<DT, true, true>(slots, p, grid_a, st) : launch_slots<DT, true, false>(slots, p, grid_a, st);
+  else e = mask ? launch_slots<DT, false, true>(slots, p, grid_a, st) : launch_slots<DT, false, false>(slots, p, grid_a, st);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((tail_kernel<DT>), dim3(grid_b), dim3(kThreads), 0, st, p);
+  return hipGetLastError();
 }
 
 }  // namespace oxs
@@ -1031,7 +1242,6 @@ struct oxs_sampler {
   uint64_t* lists;
   uint64_t* wave_theta;
   uint32_t* wave_count;
-  uint32_t* tickets;
   size_t bytes;
 };
 
@@ -1106,13 +1316,10 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
   const size_t b_lists = B * oxs::kUnionMax * sizeof(uint64_t);
   const size_t b_theta = B * W * sizeof(uint64_t);
   const size_t b_count = B * W * sizeof(uint32_t);
-  const size_t b_tick = B * sizeof(uint32_t);
-  bool ok = hipMalloc((void**)&s->lists, b_lists) == hipSuccess &&
-            hipMalloc((void**)&s->wave_theta, b_theta) == hipSuccess &&
-            hipMalloc((void**)&s->wave_count, b_count) == hipSuccess &&
-            hipMalloc((void**)&s->tickets, b_tick) == hipSuccess &&
-            hipMemset(s->tickets, 0, b_tick) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
-  s->bytes = b_lists + b_theta + b_count + b_tick;
+  const bool ok = hipMalloc((void**)&s->lists, b_lists) == hipSuccess &&
+                  hipMalloc((void**)&s->wave_theta, b_theta) == hipSuccess &&
+                  hipMalloc((void**)&s->wave_count, b_count) == hipSuccess;
+  s->bytes = b_lists + b_theta + b_count;
   if (!ok) {
     oxs_sampler_destroy(s);
     return OXS_ERR_HIP;
@@ -1126,7 +1333,6 @@ int oxs_sampler_destroy(oxs_sampler* s) {
   if (s->lists) (void)hipFree(s->lists);
   if (s->wave_theta) (void)hipFree(s->wave_theta);
   if (s->wave_count) (void)hipFree(s->wave_count);
-  if (s->tickets) (void)hipFree(s->tickets);
   free(s);
   return OXS_OK;
 }
@@ -1193,23 +1399,24 @@ int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
   p.S = g.S;
   p.CH = g.CH;
   p.cap_w = g.cap_w;
+  p.cap_shift = (uint32_t)__builtin_ctz(g.cap_w);
   p.c_w = g.c_w;
-  p.grid_real = b->batch * g.S;
-  p.grid_per_xcd = (p.grid_real + 7) / 8;
   p.lists = s->lists;
   p.wave_theta = s->wave_theta;
   p.wave_count = s->wave_count;
-  p.tickets = s->tickets;
+  // Group rows by XCD when the batch divides evenly over the 8 XCDs.
+  p.rpx = (b->batch % 8 == 0) ? b->batch / 8 : 0;
+  const uint32_t grid_a = b->batch * g.S;
+  const uint32_t grid_b = b->batch;
 
-  const size_t esz = b->logits_dtype == OXS_DTYPE_F32 ? 4 : 2;
-  const size_t epl = b->logits_dtype == OXS_DTYPE_F32 ? 4 : 8;
-  const bool vec = ((uintptr_t)b->logits % 16 == 0) && ((size_t)b->logits_ld % epl == 0) && esz > 0;
+  const uint32_t epl = b->logits_dtype == OXS_DTYPE_F32 ? 4 : 8;
+  const bool vec = ((uintptr_t)b->logits % 16 == 0) && ((size_t)b->logits_ld % epl == 0) &&
+                   (b->vocab % epl == 0);
+  const bool mask = b->allowed_mask != nullptr;
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e;
-  if (b->logits_dtype == OXS_DTYPE_F32)
-    e = vec ? launch_slots<OXS_DTYPE_F32, true>(g.slots, p, st) : launch_slots<OXS_DTYPE_F32, false>(g.slots, p, st);
-  else
-    e = vec ? launch_slots<OXS_DTYPE_BF16, true>(g.slots, p, st) : launch_slots<OXS_DTYPE_BF16, false>(g.slots, p, st);
+  const hipError_t e = b->logits_dtype == OXS_DTYPE_F32
+                           ? launch_all<OXS_DTYPE_F32>(g.slots, vec, mask, p, grid_a, grid_b, st)
+                           : launch_all<OXS_DTYPE_BF16>(g.slots, vec, mask, p, grid_a, grid_b, st);
   return e == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }
 
