@@ -122,6 +122,61 @@ def read_traffic(path):
         return None, None
 
 
+def _pmc_rows(folder, counter):
+    import csv  # noqa: PLC0415
+    files = sorted(Path(folder).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {folder}")
+    rows = []
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def _per_launch(rows):
+    """KiB per sampler launch: one stream_kernel dispatch plus the tail_kernel after it."""
+    out, cur = [], None
+    for _, name, v in rows:
+        if "oxs::" not in name:
+            continue
+        if "stream_kernel" in name:
+            cur = v
+        elif "tail_kernel" in name and cur is not None:
+            out.append(cur + v)
+            cur = None
+    if not out:
+        raise SystemExit("no sampler launches in the counter rows")
+    return float(np.median(out)), len(out)
+
+
+def _copy_kib(rows):
+    v = [val for _, name, val in rows if "copyBuffer" in name]
+    if not v:
+        raise SystemExit("no copy dispatches in the calibration rows")
+    return float(np.median(v))
+
+
+def summarize_pmc(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir):
+    """HBM bytes per launch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
+    each scaled by what the same counter reads for a plain 256 MiB device copy."""
+    copy_bytes = 256 << 20
+    f_kib, n_f = _per_launch(_pmc_rows(fetch_dir, "FETCH_SIZE"))
+    w_kib, n_w = _per_launch(_pmc_rows(write_dir, "WRITE_SIZE"))
+    cf = copy_bytes / (_copy_kib(_pmc_rows(copy_fetch_dir, "FETCH_SIZE")) * 1024)
+    cw = copy_bytes / (_copy_kib(_pmc_rows(copy_write_dir, "WRITE_SIZE")) * 1024)
+    fetch_b, write_b = f_kib * 1024 * cf, w_kib * 1024 * cw
+    return {
+        "traffic_bytes_per_launch": fetch_b + write_b,
+        "fetch_bytes_per_launch": fetch_b, "write_bytes_per_launch": write_b,
+        "fetch_kib_raw": f_kib, "write_kib_raw": w_kib,
+        "copy_scale_fetch": cf, "copy_scale_write": cw,
+        "launches_fetch": n_f, "launches_write": n_w,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,7 +189,14 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only 8 plain 256 MiB device copies (scale for the rocprofv3 byte counters)")
     ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
+    ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
+                    help="turn four rocprofv3 --pmc output folders into the traffic summary and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summary = summarize_pmc(*args.summarize_pmc)
+        Path(args.traffic_summary).write_text(json.dumps(summary, indent=1) + "\n")
+        print(json.dumps(summary), flush=True)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -284,7 +346,7 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes_per_launch": alg,
             "traffic_source": traffic_src,
-            "kernel": "oxs::sample_kernel<0,8,true>",
+            "kernel": "oxs_sample_batch = stream_kernel + tail_kernel (one launch pair, timed together)",
         },
         "wall_s": wall,
     }

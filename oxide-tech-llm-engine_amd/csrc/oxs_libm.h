@@ -13,10 +13,12 @@
 // glibc builds these routines twice on x86_64 and picks one at load time
 // (ifunc): a generic build and an FMA build in which the compiler fuses each
 // multiply feeding an add. The two builds differ in the last bit for a small
-// fraction of inputs, so both are provided here: OXS_LIBM_FMA selects the fused
-// form. The host library decides which one the host's libm uses (see
-// oxs_host_libm_variant in oxs_api.cpp) so the device matches the CPU the
-// reference sampler would run on.
+// fraction of inputs, so both are provided here (template argument FUSED).
+// The device uses the fused form: glibc selects it on every x86_64 CPU with
+// FMA, which includes every host CPU an MI355X is paired with.
+//
+// Each routine takes its table as an argument (defaulting to the constant
+// tables below) so that device code can pass copies held in LDS.
 //
 // This header compiles as HIP device code and as plain host C++ (for the
 // tests that sweep it against the host libm). Build with -ffp-contract=off.
@@ -92,7 +94,7 @@ OXS_CONST_TABLE double kLog2Logc[16] = {
 
 // expf: x*32/ln2 = k + r, exp(x) = 2^(k/32) * 2^(r/32), 2^(r/32) by a cubic.
 template <bool FUSED>
-OXS_HD float expf_t(float x) {
+OXS_HD float expf_t(float x, const uint64_t* exp2tab = kExp2Tab) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
   const double kShift = 0x1.8p+52;
   const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -124,7 +126,7 @@ OXS_HD float expf_t(float x) {
     double z = kInvLn2N * xd;
     r = z - kd;
   }
-  uint64_t t = kExp2Tab[ki % 32];
+  uint64_t t = exp2tab[ki % 32];
   t += ki << 47;
   double s = u2d(t);
   double zz = mad<FUSED>(C0, r, C1);
@@ -158,7 +160,7 @@ OXS_HD bool log_special(float x, uint32_t* ix_io, float* special) {
 }
 
 template <bool FUSED>
-OXS_HD float logf_t(float x) {
+OXS_HD float logf_t(float x, const double* invc_tab = kLogInvc, const double* logc_tab = kLnLogc) {
   const double kLn2 = 0x1.62e42fefa39efp-1;
   const double A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2, A2 = -0x1.ffffef20a4123p-2;
   uint32_t ix = f2u(x);
@@ -168,7 +170,7 @@ OXS_HD float logf_t(float x) {
   int i = (int)((tmp >> (23 - 4)) % 16);
   int k = (int32_t)tmp >> 23;
   uint32_t iz = ix - (tmp & 0xff800000u);
-  double invc = kLogInvc[i], logc = kLnLogc[i];
+  double invc = invc_tab[i], logc = logc_tab[i];
   double z = (double)u2f(iz);
   double r = mad<FUSED>(z, invc, -1.0);
   double y0 = mad<FUSED>((double)k, kLn2, logc);
@@ -180,7 +182,7 @@ OXS_HD float logf_t(float x) {
 }
 
 template <bool FUSED>
-OXS_HD float log2f_t(float x) {
+OXS_HD float log2f_t(float x, const double* invc_tab = kLogInvc, const double* logc_tab = kLog2Logc) {
   const double A0 = -0x1.712b6f70a7e4dp-2, A1 = 0x1.ecabf496832ep-2, A2 = -0x1.715479ffae3dep-1,
                A3 = 0x1.715475f35c8b8p0;
   uint32_t ix = f2u(x);
@@ -191,7 +193,7 @@ OXS_HD float log2f_t(float x) {
   uint32_t top = tmp & 0xff800000u;
   uint32_t iz = ix - top;
   int k = (int32_t)tmp >> 23;
-  double invc = kLogInvc[i], logc = kLog2Logc[i];
+  double invc = invc_tab[i], logc = logc_tab[i];
   double z = (double)u2f(iz);
   double r = mad<FUSED>(z, invc, -1.0);
   double y0 = logc + (double)k;

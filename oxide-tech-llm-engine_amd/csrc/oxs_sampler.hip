@@ -17,13 +17,14 @@
 //   candidates by value descending, then lower token id.
 //
 // tail_kernel (one block per row). Reads the row's candidate keys and the
-//   wavefront thresholds; if at least M = max(top_k, 256) keys lie at or above
-//   the largest threshold, those keys provably contain the row's top M
-//   (otherwise the block re-scans the row exactly). A bucketed counting sort
-//   yields the sorted top M, then softmax, Mirostat or min-p / XTC / top-k /
-//   tail-free / typical / top-p, renormalisation and the inverse-CDF draw run
-//   with expf/logf/log2f that reproduce glibc bit for bit and with every float
-//   sum in the reference's order.
+//   wavefront thresholds into registers; if at least M = max(top_k, 256) keys
+//   lie at or above the largest threshold, those keys provably contain the
+//   row's top M (otherwise the block re-scans the row exactly). A bucketed
+//   counting sort yields the sorted top M. One wavefront then runs softmax,
+//   Mirostat or min-p / XTC / top-k / tail-free / typical / top-p,
+//   renormalisation and the inverse-CDF draw without block barriers, with
+//   expf/logf/log2f that reproduce glibc bit for bit and with every float sum
+//   in the reference's order.
 //
 // The kernel boundary makes the candidate keys visible to the tail on every
 // XCD without per-block cache write-backs. Nothing is allocated and nothing
@@ -45,7 +46,7 @@ constexpr int kMaxM = 1024;       // largest max(top_k, 256) run on the device
 constexpr int kMaxChunk = 8192;   // logits per stream block
 constexpr int kMaxChunks = 64;    // chunks per row
 constexpr int kHashSlots = 256;   // marked (sparse-stage) ids per stream block
-constexpr int kBuckets = 1024;    // tail counting-sort buckets
+constexpr int kBuckets = 256;     // tail counting-sort buckets
 constexpr int kHistUnroll = 4;    // history ids per thread loaded ahead of the stream
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -203,23 +204,87 @@ __device__ __forceinline__ bool mask_allows(const Params& p, uint32_t row, uint3
   return (w >> (idx & 31)) & 1u;
 }
 
-// ---------------------------------------------------------------- block helpers
+// ---------------------------------------------------------------- wavefront and block helpers
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// Orders this wavefront's LDS accesses: a wavefront's LDS operations complete in
+// issue order, so a fence that stops the compiler from moving memory accesses
+// across it is all that one wavefront needs to read what its lanes wrote.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// DPP lane exchanges (gfx9 data-parallel primitives; no LDS traffic).
+// CTRL: 0xB1 quad_perm(1,0,3,2) = lane ^ 1, 0x4E quad_perm(2,3,0,1) = lane ^ 2,
+// 0x141 row_half_mirror, 0x140 row_mirror, 0x110 + k row_shr:k,
+// 0x142 row_bcast:15, 0x143 row_bcast:31.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+  return ((uint64_t)dpp32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp32<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+struct MaxOp {
+  template <typename T> __device__ T operator()(T a, T b) const { return a > b ? a : b; }
+};
+struct MinOp {
+  template <typename T> __device__ T operator()(T a, T b) const { return a < b ? a : b; }
+};
+struct AddOp {
+  template <typename T> __device__ T operator()(T a, T b) const { return a + b; }
+};
+// Reduction over the wavefront: lane ^ 1, lane ^ 2, then the mirrors pair each
+// quad with its neighbour and each half-row with the other half, so every lane
+// holds its 16-lane row's result; the four rows are combined from readlanes.
+template <typename Op>
+__device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op) {
+  v = op(v, dpp64<0xB1>(v));
+  v = op(v, dpp64<0x4E>(v));
+  v = op(v, dpp64<0x141>(v));
+  v = op(v, dpp64<0x140>(v));
+  return op(op(readlane64(v, 0), readlane64(v, 16)), op(readlane64(v, 32), readlane64(v, 48)));
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce32(uint32_t v, Op op) {
+  v = op(v, dpp32<0xB1>(v));
+  v = op(v, dpp32<0x4E>(v));
+  v = op(v, dpp32<0x141>(v));
+  v = op(v, dpp32<0x140>(v));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return op(op(r0, r1), op(r2, r3));
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return wave_reduce64(v, MaxOp{}); }
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) { return wave_reduce64(v, MinOp{}); }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_reduce32(v, MaxOp{}); }
+// Inclusive prefix sum over the wavefront's lanes: shifts by 1, 2, 4, 8 inside
+// each 16-lane row (zeros shifted in), then row totals broadcast forward.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);
+  return x;
+}
+// Number of set bits of m below this lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
 // Exclusive prefix sum over the block; *total gets the block sum.
 __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scratch) {
   const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= (uint32_t)o) x += y;
-  }
+  const uint32_t x = wave_incl_scan(v);
   if (lane == 63) scratch[w] = x;
   __syncthreads();
   uint32_t before = 0, tot = 0;
@@ -232,22 +297,6 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scrat
   __syncthreads();
   *total = tot;
   return x - v + before;
-}
-
-template <bool MAX>
-__device__ uint64_t block_reduce_u64(uint64_t v, uint64_t* scratch) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t y = __shfl_xor(v, o, 64);
-    v = MAX ? (y > v ? y : v) : (y < v ? y : v);
-  }
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint64_t m = scratch[0];
-#pragma unroll
-  for (int i = 1; i < kWavesPerBlock; ++i) m = MAX ? (scratch[i] > m ? scratch[i] : m) : (scratch[i] < m ? scratch[i] : m);
-  __syncthreads();
-  return m;
 }
 
 // ---------------------------------------------------------------- marked-id hash (LDS)
@@ -516,12 +565,11 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
 // ---------------------------------------------------------------- tail helpers
 
 struct TailShared {
-  uint32_t wcnt[kMaxChunks * kWavesPerBlock];
+  uint64_t a_theta[kWavesPerBlock];  // per-wavefront partials of the first reduction
+  uint64_t a_kmax[kWavesPerBlock];
+  uint64_t a_kmin[kWavesPerBlock];
   uint32_t scan_scratch[8];
-  uint64_t red_scratch[8];
   uint32_t sel_digit, sel_above, sel_count, counter;
-  uint32_t n, token, first;
-  float f;
 };
 
 // Sorts n keys in LDS descending (ascending if ASC), padding to a power of two.
@@ -672,92 +720,34 @@ __device__ uint32_t exact_select_row(const Params& p, const RowXf& r, uint32_t r
 
 __device__ __forceinline__ float key_value(uint64_t k) { return ord2f((uint32_t)(k >> 32)); }
 
-// The M largest of n distinct keys u[0..n), sorted descending, into out[0..M).
-// Counting sort over kBuckets buckets that are linear in the float value
-// between the smallest and largest key (rounded subtraction and scaling are
-// monotone, so bucket order agrees with key order), then the exact order
-// inside each bucket by rank. Falls back to a bitonic sort of all n keys when
-// the values are not finite or one needed bucket holds many keys.
-__device__ void select_sorted(uint64_t* u, uint32_t n, uint32_t M, uint64_t* out, uint64_t* tmp,
-                              uint32_t* bstart, uint32_t* bfill, TailShared& ts) {
-  const uint32_t tid = threadIdx.x;
-  uint64_t kmx = 0, kmn = ~0ull;
-  for (uint32_t i = tid; i < n; i += kThreads) {
-    const uint64_t k = u[i];
-    kmx = k > kmx ? k : kmx;
-    kmn = k < kmn ? k : kmn;
-  }
-  const float vmax = key_value(block_reduce_u64<true>(kmx, ts.red_scratch));
-  const float vmin = key_value(block_reduce_u64<false>(kmn, ts.red_scratch));
-  const float range = vmax - vmin;
-  const float scale = (float)(kBuckets - 1) / range;
-  const bool linear = range > 0.0f && range <= __FLT_MAX__ && scale <= __FLT_MAX__ &&
-                      vmax <= __FLT_MAX__ && vmin >= -__FLT_MAX__;
-  bool fallback = !linear;
-  uint32_t span = 0;
-  if (linear) {
-    for (uint32_t b = tid; b < (uint32_t)kBuckets; b += kThreads) bfill[b] = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < n; i += kThreads) {
-      const uint32_t b = min((uint32_t)((vmax - key_value(u[i])) * scale), (uint32_t)kBuckets - 1);
-      atomicAdd(&bfill[b], 1u);
-    }
-    __syncthreads();
-    static_assert(kBuckets == 4 * kThreads, "4 buckets per thread");
-    uint32_t c4[4], loc = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = bfill[tid * 4 + q];
-      loc += c4[q];
-    }
-    uint32_t total;
-    uint32_t run = block_excl_scan(loc, &total, ts.scan_scratch);
-    uint32_t mxb = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      bstart[tid * 4 + q] = run;
-      if (run < M) mxb = c4[q] > mxb ? c4[q] : mxb;  // largest needed bucket
-      if (run < M && run + c4[q] >= M) ts.sel_digit = tid * 4 + q;  // bucket of the M-th key
-      run += c4[q];
-    }
-    const uint32_t big = (uint32_t)block_reduce_u64<true>(mxb, ts.red_scratch);
-    const uint32_t last = ts.sel_digit;
-    span = last + 1 < (uint32_t)kBuckets ? bstart[last + 1] : total;  // keys in buckets <= last
-    fallback = big > 64 || span > 2u * kMaxM;
-    if (!fallback) {
-      for (uint32_t b = tid; b < (uint32_t)kBuckets; b += kThreads) bfill[b] = bstart[b];
-      __syncthreads();
-      for (uint32_t i = tid; i < n; i += kThreads) {
-        const uint64_t k = u[i];
-        const uint32_t b = min((uint32_t)((vmax - key_value(k)) * scale), (uint32_t)kBuckets - 1);
-        if (b <= last) tmp[atomicAdd(&bfill[b], 1u)] = k;
-      }
-      __syncthreads();
-      for (uint32_t i = tid; i < span; i += kThreads) {
-        const uint64_t k = tmp[i];
-        const uint32_t b = min((uint32_t)((vmax - key_value(k)) * scale), (uint32_t)kBuckets - 1);
-        const uint32_t lo = bstart[b], hi = bfill[b];
-        uint32_t rank = lo;
-        for (uint32_t j = lo; j < hi; ++j) rank += tmp[j] > k ? 1u : 0u;
-        if (rank < M) out[rank] = k;
-      }
-      __syncthreads();
-      return;
-    }
-  }
-  bitonic_sort<false>(u, n);
-  for (uint32_t i = tid; i < M; i += kThreads) out[i] = u[i];
-  __syncthreads();
-}
-
 // ---------------------------------------------------------------- tail math
 
-using oxs_libm::expf_t;
-using oxs_libm::log2f_t;
-using oxs_libm::logf_t;
-__device__ __forceinline__ float dexpf(float x) { return expf_t<true>(x); }
-__device__ __forceinline__ float dlogf(float x) { return logf_t<true>(x); }
-__device__ __forceinline__ float dlog2f(float x) { return log2f_t<true>(x); }
+// The glibc-exact exp/ln/log2 tables, copied into LDS at tail start so the
+// chain's lookups are LDS reads rather than global-memory round trips.
+struct LibmTables {
+  uint64_t exp2[32];
+  double invc[16];
+  double lnc[16];
+  double log2c[16];
+};
+
+__device__ __forceinline__ void load_libm_tables(LibmTables& t) {
+  const uint32_t tid = threadIdx.x;
+  if (tid < 32) t.exp2[tid] = oxs_libm::kExp2Tab[tid];
+  else if (tid < 48) t.invc[tid - 32] = oxs_libm::kLogInvc[tid - 32];
+  else if (tid < 64) t.lnc[tid - 48] = oxs_libm::kLnLogc[tid - 48];
+  else if (tid < 80) t.log2c[tid - 64] = oxs_libm::kLog2Logc[tid - 64];
+}
+
+__device__ __forceinline__ float dexpf(float x, const LibmTables& t) {
+  return oxs_libm::expf_t<true>(x, t.exp2);
+}
+__device__ __forceinline__ float dlogf(float x, const LibmTables& t) {
+  return oxs_libm::logf_t<true>(x, t.invc, t.lnc);
+}
+__device__ __forceinline__ float dlog2f(float x, const LibmTables& t) {
+  return oxs_libm::log2f_t<true>(x, t.invc, t.log2c);
+}
 
 __device__ __forceinline__ float next_f32(uint64_t* s) {  // sampler.rs:139-153
   uint64_t x = *s;
@@ -769,49 +759,6 @@ __device__ __forceinline__ float next_f32(uint64_t* s) {  // sampler.rs:139-153
   return (float)val / 16777216.0f;
 }
 
-// The reference's ordered f32 running sums, computed by one thread from
-// registers: 64 values at a time are read with 16-byte LDS loads, then added
-// in index order. Adds f(a[i]) for i = 0, 1, ... to `init` and stops after the
-// first i whose running sum reaches `stop` (when USE_STOP) or at n; returns
-// that index + 1 (n when it never stops) and the running sum. `a` must be
-// 16-byte aligned and readable up to the next multiple of 64 entries.
-struct Chain {
-  uint32_t stop;
-  float sum;
-};
-
-template <bool USE_STOP, typename F>
-__device__ __noinline__ Chain lane_chain(const float* a, uint32_t n, float init, float stop, F f) {
-  float s = init;
-  for (uint32_t base = 0; base < n; base += 64) {
-    float v[64];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const float4 t = *(const float4*)(a + base + 4 * q);
-      v[4 * q] = t.x;
-      v[4 * q + 1] = t.y;
-      v[4 * q + 2] = t.z;
-      v[4 * q + 3] = t.w;
-    }
-    if (base + 64 <= n) {
-#pragma unroll
-      for (int j = 0; j < 64; ++j) {
-        s += f(v[j]);
-        if (USE_STOP && s >= stop) return Chain{base + j + 1, s};
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 64; ++j) {
-        if (base + j < n) {
-          s += f(v[j]);
-          if (USE_STOP && s >= stop) return Chain{base + j + 1, s};
-        }
-      }
-    }
-  }
-  return Chain{n, s};
-}
-
 struct Ident {
   __device__ float operator()(float v) const { return v; }
 };
@@ -820,30 +767,117 @@ struct Scaled {
   __device__ float operator()(float v) const { return v * k; }
 };
 
-// Stable block-wide compaction of (ids, pr)[0..n) keeping keep(i); returns the count.
+struct Chain {
+  uint32_t stop;  // index + 1 of the element that reached the stop value, else n
+  float sum;      // running sum there, else the total
+  bool hit;
+};
+
+__device__ __forceinline__ float4 ld4(const float* a) { return *(const float4*)a; }
+
+// 16 ordered adds of one group; t[j] is the running sum after element j.
 template <typename F>
-__device__ uint32_t compact_stable(uint32_t* ids, float* pr, uint32_t* ids2, float* pr2, uint32_t n,
-                                   F keep, TailShared& ts) {
-  const uint32_t tid = threadIdx.x;
+__device__ __forceinline__ float add16(float x, float4 q0, float4 q1, float4 q2, float4 q3, F f,
+                                       float (&t)[16]) {
+  const float v[16] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w,
+                       q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    x = x + f(v[j]);
+    t[j] = x;
+  }
+  return x;
+}
+
+// First j < lim with t[j] >= stop (16 when none): one lane stores the group's
+// running sums, sixteen lanes test one each.
+__device__ __forceinline__ uint32_t first_hit16(const float (&t)[16], uint32_t lim, float stop, float* hit,
+                                                float* at) {
+  const uint32_t l = threadIdx.x & 63;
+  if (l == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *(float4*)(hit + 4 * q) = make_float4(t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]);
+  }
+  wave_sync();
+  const float mine = hit[l & 15u];
+  const uint64_t m = __ballot(l < lim && mine >= stop);
+  uint32_t j = 16;
+  if (m) {
+    j = (uint32_t)__builtin_ctzll(m);
+    *at = hit[j];
+  }
+  wave_sync();
+  return j;
+}
+
+// The reference's ordered f32 running sum init + f(a[0]) + f(a[1]) + ...,
+// computed by every lane of one wavefront from broadcast LDS reads, 16 values
+// per group with the next group read ahead. With STOP it ends at the first
+// index whose running sum is >= stop. A group is searched only when its last
+// running sum is not below stop: the addends are >= 0, so the running sum never
+// decreases and a group without a hit ends below stop (a NaN sum sends the
+// group to the search, which finds no hit, as the reference's comparisons find
+// none). The final partial group adds -0.0 in place of the missing elements,
+// which leaves every float unchanged. `a` is 16-byte aligned and readable 16
+// entries past n; `hit` is 16 floats of LDS.
+template <bool STOP, typename F>
+__device__ __forceinline__ Chain seq_chain(const float* a, uint32_t n, float init, float stop, F f, float* hit) {
+  float s = init;
+  if (n == 0) return Chain{0u, s, false};
+  const uint32_t full = n & ~15u;
+  float4 p0 = ld4(a), p1 = ld4(a + 4), p2 = ld4(a + 8), p3 = ld4(a + 12);
   uint32_t base = 0;
-  for (uint32_t r0 = 0; r0 < n; r0 += kThreads) {
-    const uint32_t i = r0 + tid;
-    const bool k = i < n && keep(i);
-    uint32_t tot;
-    const uint32_t pos = base + block_excl_scan(k ? 1u : 0u, &tot, ts.scan_scratch);
-    if (k) {
-      ids2[pos] = ids[i];
-      pr2[pos] = pr[i];
+  float t[16];
+  float at = 0.0f;
+  for (; base + 32 <= full; base += 32) {
+    const float4 r0 = ld4(a + base + 16), r1 = ld4(a + base + 20), r2 = ld4(a + base + 24), r3 = ld4(a + base + 28);
+    __builtin_amdgcn_sched_barrier(0);
+    s = add16(s, p0, p1, p2, p3, f, t);
+    if (STOP && !(s < stop)) {
+      const uint32_t j = first_hit16(t, 16u, stop, hit, &at);
+      if (j < 16) return Chain{base + j + 1, at, true};
     }
-    base += tot;
+    __builtin_amdgcn_sched_barrier(0);
+    p0 = ld4(a + base + 32);
+    p1 = ld4(a + base + 36);
+    p2 = ld4(a + base + 40);
+    p3 = ld4(a + base + 44);
+    __builtin_amdgcn_sched_barrier(0);
+    s = add16(s, r0, r1, r2, r3, f, t);
+    if (STOP && !(s < stop)) {
+      const uint32_t j = first_hit16(t, 16u, stop, hit, &at);
+      if (j < 16) return Chain{base + 16 + j + 1, at, true};
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __syncthreads();
-  for (uint32_t i = tid; i < base; i += kThreads) {
-    ids[i] = ids2[i];
-    pr[i] = pr2[i];
+  if (base < full) {
+    s = add16(s, p0, p1, p2, p3, f, t);
+    if (STOP && !(s < stop)) {
+      const uint32_t j = first_hit16(t, 16u, stop, hit, &at);
+      if (j < 16) return Chain{base + j + 1, at, true};
+    }
+    base += 16;
+    p0 = ld4(a + base);
+    p1 = ld4(a + base + 4);
+    p2 = ld4(a + base + 8);
+    p3 = ld4(a + base + 12);
   }
-  __syncthreads();
-  return base;
+  if (base < n) {
+    const uint32_t rem = n - base;
+    const float v[16] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w,
+                         p2.x, p2.y, p2.z, p2.w, p3.x, p3.y, p3.z, p3.w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float add = (uint32_t)j < rem ? f(v[j]) : -0.0f;
+      s = s + add;
+      t[j] = s;
+    }
+    if (STOP && !(s < stop)) {
+      const uint32_t j = first_hit16(t, rem, stop, hit, &at);
+      if (j < 16) return Chain{base + j + 1, at, true};
+    }
+  }
+  return Chain{n, s, false};
 }
 
 __device__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status) {
@@ -854,90 +888,153 @@ __device__ void write_row_result(const Params& p, uint32_t row, uint32_t token, 
   }
 }
 
-// Moves (ids, pr)[from .. from+len) to [0, len) through the spare arrays.
-__device__ void shift_down(uint32_t* ids, float* pr, uint32_t* ids2, float* pr2, uint32_t from,
-                           uint32_t len) {
-  for (uint32_t i = threadIdx.x; i < len; i += kThreads) {
-    ids2[i] = ids[from + i];
-    pr2[i] = pr[from + i];
+// LDS arrays of the chain; each is readable 16 entries past kMaxM.
+constexpr int kChainLd = kMaxM + 16;
+struct ChainBufs {
+  uint32_t* ids;  // the candidates, sorted, and their exps on entry
+  float* pr;
+  uint32_t* ids_b;
+  float* pr_b;
+  float* aux;
+  uint64_t* aux64;
+  float* hit;  // 16 floats
+};
+
+// Per-row values the chain needs from global memory, read at tail start.
+struct RowState {
+  float uniform;
+  float mu;
+  uint64_t rng;
+  uint32_t history_len;
+};
+
+// Stable in-place compaction of (ids, pr)[0..len) by one wavefront: a step
+// reads 4 x 64 entries, keeps those with keep(v), and writes them below the
+// step, after all of its reads. v = xf(pr[i]) is what is kept.
+template <typename X, typename K>
+__device__ __forceinline__ uint32_t wave_compact(uint32_t* ids, float* pr, uint32_t len, X xf, K keep) {
+  const uint32_t l = threadIdx.x;
+  uint32_t kept = 0;
+  for (uint32_t r0 = 0; r0 < len; r0 += 256) {
+    uint32_t id[4];
+    float v[4];
+    uint64_t m[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {  // unconditional reads (clamped index)
+      const uint32_t i = r0 + 64u * t + l;
+      const uint32_t at = i < len ? i : 0u;
+      id[t] = ids[at];
+      v[t] = xf(pr[at]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) m[t] = __ballot(r0 + 64u * t + l < len && keep(v[t]));
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if ((m[t] >> l) & 1u) {
+        const uint32_t at = kept + lanes_below(m[t]);
+        ids[at] = id[t];
+        pr[at] = v[t];
+      }
+      kept += (uint32_t)__popcll(m[t]);
+    }
+    wave_sync();
   }
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < len; i += kThreads) {
-    ids[i] = ids2[i];
-    pr[i] = pr2[i];
-  }
-  __syncthreads();
+  return kept;
 }
 
-// The chain after the top-M selection (sampler.rs:286-389) on keys[0..n),
-// sorted descending. ids/pr/ids2/pr2 hold kMaxM entries each (contiguous, in
-// that order); aux holds 2 * kMaxM keys. Parallel stages use the whole block;
-// the reference's ordered f32 sums run in thread 0 (lane_chain).
-__device__ void tail_chain(const Params& p, const oxs_sampling_config& c, uint32_t row,
-                           const uint64_t* keys, uint32_t n, uint32_t* ids, float* pr,
-                           uint32_t* ids2, float* pr2, uint64_t* aux, TailShared& ts) {
-  const uint32_t tid = threadIdx.x;
-  // Softmax over the n kept candidates (:286-295).
-  const float max_logit = key_value(keys[0]);
-  for (uint32_t i = tid; i < n; i += kThreads) {
-    const uint64_t k = keys[i];
-    ids[i] = ~(uint32_t)k;
-    pr[i] = dexpf(key_value(k) - max_logit);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    const float sum_exp = lane_chain<false>(pr, n, 0.0f, 0.0f, Ident{}).sum;
-    ts.f = sum_exp > 0.0f ? 1.0f / sum_exp : 1.0f;
-  }
-  __syncthreads();
-  const float inv_sum = ts.f;
-  for (uint32_t i = tid; i < n; i += kThreads) pr[i] *= inv_sum;
-  __syncthreads();
+// The chain after the top-M selection (sampler.rs:286-389) on the n
+// candidates in bf.ids, sorted, with bf.pr = exp(logit - max logit) (the
+// softmax numerators, :286-290), run by one wavefront (threads 0..63) with no
+// block barriers: parallel stages split the candidates over the lanes; the
+// reference's ordered sums run in every lane at once (seq_chain), so each lane
+// holds each result.
+__device__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32_t row, uint32_t n,
+                           ChainBufs bf, const RowState& rs, const LibmTables& tab) {
+  const uint32_t l = threadIdx.x;
+  uint32_t* ids = bf.ids;
+  float* pr = bf.pr;
+  // Softmax normalisation (:291-295): the scaling by 1 / sum is applied by the
+  // next pass that reads the numerators.
+  const float sum_exp = seq_chain<false>(pr, n, 0.0f, 0.0f, Ident{}, bf.hit).sum;
+  const float inv_sum = sum_exp > 0.0f ? 1.0f / sum_exp : 1.0f;
+  const Scaled to_prob{inv_sum};
 
-  uint32_t len = n, n_record = 1;
-  if (c.mirostat_mode == OXS_MIROSTAT_V1 || c.mirostat_mode == OXS_MIROSTAT_V2) {
-    const float mu0 = p.mu[row];
-    if (c.mirostat_mode == OXS_MIROSTAT_V2) {  // :432-456
-      // the included prefix ends before the first i > 0 whose surprise exceeds mu
-      if (tid == 0) ts.first = n;
-      __syncthreads();
-      for (uint32_t i = tid; i < n; i += kThreads) {
-        const float surprise = -dlog2f(fmaxf(pr[i], 1e-8f));
-        if (i > 0 && surprise > mu0) atomicMin(&ts.first, i);
+  uint32_t len = n, n_record = 1, token;
+  float inv_total = 1.0f;
+  const bool mirostat = c.mirostat_mode == OXS_MIROSTAT_V1 || c.mirostat_mode == OXS_MIROSTAT_V2;
+  // Min-p (:315-319): keep p >= p_max * min_p, in order; the pass also turns
+  // the exps into probabilities.
+  if (!mirostat && c.min_p > 0.0f && len > 0) {
+    const float threshold = to_prob(pr[0]) * c.min_p;
+    len = wave_compact(ids, pr, len, to_prob, [=](float v) { return v >= threshold; });
+  } else {
+    for (uint32_t r0 = 0; r0 < n; r0 += 256) {
+      float v[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t i = r0 + 64u * t + l;
+        v[t] = pr[i < n ? i : 0u];
       }
-      __syncthreads();
-    }
-    if (tid == 0) {
-      float mu = mu0;
-      if (c.mirostat_mode == OXS_MIROSTAT_V1) {  // :418-429
-        const float prob = fmaxf(pr[0], 1e-6f);
-        const float surprise = -dlog2f(prob);
-        const float error = surprise - c.mirostat_tau;
-        const float step = c.mirostat_eta * error;
-        mu -= step;
-      } else {
-        const float cum_prob = lane_chain<false>(pr, ts.first, 0.0f, 0.0f, Ident{}).sum;
-        const float prob = pr[0] / fmaxf(cum_prob, 1e-6f);
-        const float surprise = -dlog2f(fmaxf(prob, 1e-8f));
-        const float error = surprise - c.mirostat_tau;
-        const float step = c.mirostat_eta * error;
-        mu -= step;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t i = r0 + 64u * t + l;
+        if (i < n) pr[i] = to_prob(v[t]);
       }
-      p.mu[row] = mu;
-      ts.token = ids[0];
     }
+    wave_sync();
+  }
+
+  if (mirostat) {
+    const float mu0 = rs.mu;
+    float mu = mu0;
+    if (c.mirostat_mode == OXS_MIROSTAT_V1) {  // :418-429
+      const float prob = fmaxf(pr[0], 1e-6f);
+      const float surprise = -dlog2f(prob, tab);
+      const float error = surprise - c.mirostat_tau;
+      const float step = c.mirostat_eta * error;
+      mu -= step;
+    } else {  // :432-456: the prefix ends before the first i > 0 whose surprise exceeds mu
+      uint32_t first = n;
+      for (uint32_t r0 = 0; r0 < n; r0 += 64) {
+        const uint32_t i = r0 + l;
+        const bool over = i < n && i > 0 && -dlog2f(fmaxf(pr[i], 1e-8f), tab) > mu0;
+        const uint64_t m = __ballot(over);
+        if (m) {
+          first = r0 + (uint32_t)__builtin_ctzll(m);
+          break;
+        }
+      }
+      const float cum_prob = seq_chain<false>(pr, first, 0.0f, 0.0f, Ident{}, bf.hit).sum;
+      const float prob = pr[0] / fmaxf(cum_prob, 1e-6f);
+      const float surprise = -dlog2f(fmaxf(prob, 1e-8f), tab);
+      const float error = surprise - c.mirostat_tau;
+      const float step = c.mirostat_eta * error;
+      mu -= step;
+    }
+    if (l == 0) p.mu[row] = mu;
+    token = ids[0];
     n_record = 2;  // recorded inside the mode function and by the caller (:301, :307)
   } else {
-    // Min-p (:315-319): keep p >= p_max * min_p, in order.
-    if (c.min_p > 0.0f && len > 0) {
-      const float threshold = pr[0] * c.min_p;
-      len = compact_stable(ids, pr, ids2, pr2, len, [=](uint32_t i) { return pr[i] >= threshold; }, ts);
-    }
     // XTC (:322-328): drop the top choice.
     if (c.xtc_probability > 0.0f && len > 1) {
       const float p_max = pr[0];
       if (p_max >= c.xtc_threshold && p_max < 0.98f) {
-        shift_down(ids, pr, ids2, pr2, 1, len - 1);
+        for (uint32_t r0 = 0; r0 + 1 < len; r0 += 64) {
+          const uint32_t i = r0 + 1 + l;
+          uint32_t id = 0;
+          float v = 0.0f;
+          if (i < len) {
+            id = ids[i];
+            v = pr[i];
+          }
+          wave_sync();
+          if (i < len) {
+            ids[i - 1] = id;
+            pr[i - 1] = v;
+          }
+          wave_sync();
+        }
         len -= 1;
       }
     }
@@ -945,101 +1042,97 @@ __device__ void tail_chain(const Params& p, const oxs_sampling_config& c, uint32
     if (c.top_k > 0 && len > c.top_k) len = c.top_k;
     // Tail-free (:336-338, :459-490).
     if (c.tfs_z < 1.0f && len > 2) {
-      float* d2 = pr2;
+      float* d2 = bf.aux;
       const uint32_t m = len - 2;
-      for (uint32_t i = tid; i < m; i += kThreads) {
+      for (uint32_t i = l; i < m; i += 64) {
         const float d1a = pr[i] - pr[i + 1];
         const float d1b = pr[i + 1] - pr[i + 2];
         d2[i] = fabsf(d1a - d1b);
       }
-      __syncthreads();
-      if (tid == 0) {
-        const float sum_d2 = lane_chain<false>(d2, m, 0.0f, 0.0f, Ident{}).sum;
-        uint32_t keep = len;
-        if (sum_d2 > 0.0f) {
-          const float inv = 1.0f / sum_d2;
-          const Chain ch = lane_chain<true>(d2, m, 0.0f, c.tfs_z, Scaled{inv});
-          const uint32_t cutoff = ch.stop < m || ch.sum >= c.tfs_z ? ch.stop : len;
-          keep = cutoff > 1 ? cutoff : 1;
-        }
-        ts.n = keep;
+      wave_sync();
+      const float sum_d2 = seq_chain<false>(d2, m, 0.0f, 0.0f, Ident{}, bf.hit).sum;
+      uint32_t keep = len;
+      if (sum_d2 > 0.0f) {
+        const float inv = 1.0f / sum_d2;
+        const Chain ch = seq_chain<true>(d2, m, 0.0f, c.tfs_z, Scaled{inv}, bf.hit);
+        const uint32_t cutoff = ch.hit ? ch.stop : len;
+        keep = cutoff > 1 ? cutoff : 1;
       }
-      __syncthreads();
-      len = ts.n;
+      len = keep;
     }
-    // Locally typical (:341-343, :493-520): stable sort by |surprisal - H|.
+    // Locally typical (:341-343, :493-520): stable sort by |surprisal - H|,
+    // by rank counting over (score, position) keys.
     if (c.typical_p < 1.0f && len > 1) {
-      float* terms = pr2;
-      for (uint32_t i = tid; i < len; i += kThreads) terms[i] = pr[i] > 0.0f ? (-pr[i]) * dlogf(pr[i]) : 0.0f;
-      __syncthreads();
-      if (tid == 0) ts.f = lane_chain<false>(terms, len, -0.0f, 0.0f, Ident{}).sum;
-      __syncthreads();
-      const float entropy = ts.f;
-      for (uint32_t i = tid; i < len; i += kThreads) {
-        const float surprisal = pr[i] > 0.0f ? -dlogf(pr[i]) : 0.0f;
+      float* terms = bf.aux;
+      uint64_t* sk = bf.aux64;
+      for (uint32_t i = l; i < len; i += 64) terms[i] = pr[i] > 0.0f ? (-pr[i]) * dlogf(pr[i], tab) : 0.0f;
+      wave_sync();
+      const float entropy = seq_chain<false>(terms, len, -0.0f, 0.0f, Ident{}, bf.hit).sum;
+      for (uint32_t i = l; i < len; i += 64) {
+        const float surprisal = pr[i] > 0.0f ? -dlogf(pr[i], tab) : 0.0f;
         const float diff = fabsf(surprisal - entropy);
-        aux[i] = ((uint64_t)f2ord(diff) << 32) | i;  // ascending score, then position
+        sk[i] = ((uint64_t)f2ord(diff) << 32) | i;  // ascending score, then position
       }
-      __syncthreads();
-      bitonic_sort<true>(aux, len);
-      for (uint32_t i = tid; i < len; i += kThreads) {
-        const uint32_t src = (uint32_t)aux[i];
-        ids2[i] = ids[src];
-        pr2[i] = pr[src];
-      }
-      __syncthreads();
-      for (uint32_t i = tid; i < len; i += kThreads) {
-        ids[i] = ids2[i];
-        pr[i] = pr2[i];
-      }
-      __syncthreads();
-      if (tid == 0) ts.n = lane_chain<true>(pr, len, 0.0f, c.typical_p, Ident{}).stop;
-      __syncthreads();
-      len = ts.n;
-    }
-    if (tid == 0) {
-      // Top-p (:346-357): cut at the first running sum >= top_p.
-      uint32_t cut = len;
-      if (c.top_p < 1.0f) cut = lane_chain<true>(pr, len, 0.0f, c.top_p, Ident{}).stop;
-      // Renormalise (:360-368).
-      const float total = lane_chain<false>(pr, cut, -0.0f, 0.0f, Ident{}).sum;
-      ts.f = total > 0.0f ? 1.0f / total : 1.0f;
-      ts.n = cut;
-    }
-    __syncthreads();
-    len = ts.n;
-    const float inv_total = ts.f;
-    for (uint32_t i = tid; i < len; i += kThreads) pr[i] *= inv_total;
-    __syncthreads();
-    if (tid == 0) {
-      // Draw (:371-385): greedy below 1e-6, else the first running sum >= r;
-      // the fallback is the first candidate.
-      uint32_t picked;
-      if (c.temperature <= 1e-6f) {
-        picked = len ? ids[0] : 0u;
-      } else {
-        float rnd;
-        if (p.uniforms) {
-          rnd = p.uniforms[row];
-        } else {
-          uint64_t st = p.rng_state[row];
-          rnd = next_f32(&st);
-          p.rng_state[row] = st;
+      if (l == 0) sk[len] = ~0ull;  // pad for the pairwise reads below
+      wave_sync();
+      for (uint32_t g = 0; g < len; g += 256) {
+        uint64_t mine[4];
+        uint32_t rank[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t i = g + l + 64u * t;
+          mine[t] = i < len ? sk[i] : 0ull;
+          rank[t] = 0;
         }
-        const Chain ch = lane_chain<true>(pr, len, 0.0f, rnd, Ident{});
-        const bool hit = len > 0 && ch.sum >= rnd && ch.stop >= 1;
-        picked = hit ? ids[ch.stop - 1] : (len ? ids[0] : 0u);
+        for (uint32_t j = 0; j < len; j += 2) {
+          const uint64_t a0 = sk[j], a1 = sk[j + 1];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) rank[t] += (a0 < mine[t] ? 1u : 0u) + (a1 < mine[t] ? 1u : 0u);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t i = g + l + 64u * t;
+          if (i < len) {
+            bf.ids_b[rank[t]] = ids[i];
+            bf.pr_b[rank[t]] = pr[i];
+          }
+        }
       }
-      ts.token = picked;
+      wave_sync();
+      ids = bf.ids_b;
+      pr = bf.pr_b;
+      len = seq_chain<true>(pr, len, 0.0f, c.typical_p, Ident{}, bf.hit).stop;
+    }
+    // Top-p (:346-357) cuts at the first running sum >= top_p; the
+    // renormalisation total (:360-368) is the running sum at that cut.
+    {
+      const Chain ch = c.top_p < 1.0f ? seq_chain<true>(pr, len, 0.0f, c.top_p, Ident{}, bf.hit)
+                                      : seq_chain<false>(pr, len, 0.0f, 0.0f, Ident{}, bf.hit);
+      len = ch.stop;
+      inv_total = ch.sum > 0.0f ? 1.0f / ch.sum : 1.0f;
+    }
+    // Draw (:371-385) over the renormalised p: greedy below 1e-6, else the
+    // first running sum >= r; the fallback is the first candidate.
+    if (c.temperature <= 1e-6f) {
+      token = len ? ids[0] : 0u;
+    } else {
+      float rnd;
+      if (p.uniforms) {
+        rnd = rs.uniform;
+      } else {
+        uint64_t st = rs.rng;
+        rnd = next_f32(&st);
+        if (l == 0) p.rng_state[row] = st;
+      }
+      const Chain ch = seq_chain<true>(pr, len, 0.0f, rnd, Scaled{inv_total}, bf.hit);
+      token = ch.hit ? ids[ch.stop - 1] : (len ? ids[0] : 0u);
     }
   }
-  __syncthreads();
-  const uint32_t token = ts.token;
   // Outputs: token, status, history, candidates_buffer.
-  if (tid == 0) {
+  if (l == 0) {
     int32_t status = OXS_ROW_OK;
     if (p.flags & OXS_FLAG_RECORD_HISTORY) {
-      uint32_t hl = p.history_len[row];
+      uint32_t hl = rs.history_len;
       for (uint32_t k = 0; k < n_record; ++k) {
         if (hl < p.history_cap) {
           p.history[(size_t)row * p.history_ld + hl] = token;
@@ -1055,27 +1148,102 @@ __device__ void tail_chain(const Params& p, const oxs_sampling_config& c, uint32
     if (p.out_kept_count) p.out_kept_count[row] = len;
   }
   const uint32_t nk = (uint32_t)min((int64_t)len, p.kept_ld);
-  for (uint32_t i = tid; i < nk; i += kThreads) {
+  for (uint32_t i = l; i < nk; i += 64) {
     if (p.out_kept_ids) p.out_kept_ids[(size_t)row * p.kept_ld + i] = ids[i];
-    if (p.out_kept_probs) p.out_kept_probs[(size_t)row * p.kept_ld + i] = pr[i];
+    if (p.out_kept_probs) p.out_kept_probs[(size_t)row * p.kept_ld + i] = pr[i] * inv_total;
   }
+}
+
+// ---------------------------------------------------------------- top-M selection
+
+constexpr int kPer = kUnionMax / kThreads;  // candidate key slots per tail thread
+constexpr uint32_t kBigBucket = 64;         // largest bucket ranked by direct comparison
+static_assert(kBuckets == 4 * 64, "4 buckets per lane of a scanning wavefront");
+
+__device__ __forceinline__ uint32_t bucket_of(uint64_t k, float vmax, float scale) {
+  return min((uint32_t)((vmax - key_value(k)) * scale), (uint32_t)kBuckets - 1);
+}
+
+// Fallback selection: all kept register keys (bit q of vm) into tmp, a bitonic
+// sort, the first meff into out. Returns the number of kept keys.
+__device__ uint32_t sort_select(const uint64_t (&lk)[kPer], uint32_t vm, uint32_t M, uint64_t* tmp,
+                                uint64_t* out, TailShared& ts) {
+  const uint32_t cnt = (uint32_t)__popc(vm);
+  uint32_t n;
+  uint32_t pos = block_excl_scan(cnt, &n, ts.scan_scratch);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q)
+    if ((vm >> q) & 1u) tmp[pos++] = lk[q];
+  __syncthreads();
+  const uint32_t meff = min(M, n);
+  if (meff == 0) return 0;
+  bitonic_sort<false>(tmp, n);
+  for (uint32_t i = threadIdx.x; i < meff; i += kThreads) out[i] = tmp[i];
+  __syncthreads();
+  return n;
 }
 
 // ---------------------------------------------------------------- tail kernel
 
+// ids / exps of sorted keys[0..n) (n >= 1) into the chain arrays; ends with a barrier.
+__device__ void keys_to_chain(const uint64_t* keys, uint32_t n, uint32_t* ids, float* pr, const LibmTables& tab) {
+  const float max_logit = key_value(keys[0]);
+  for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+    const uint64_t k = keys[i];
+    ids[i] = ~(uint32_t)k;
+    pr[i] = dexpf(key_value(k) - max_logit, tab);
+  }
+  __syncthreads();
+}
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
-  __shared__ __align__(16) uint64_t smem_u[kUnionMax];  // candidate keys / exact-path table / chain arrays
-  __shared__ __align__(16) uint64_t smem_k[kMaxM];      // sorted top-M keys
-  __shared__ __align__(16) uint64_t smem_t[2 * kMaxM];  // counting-sort scatter / typical-sort keys
-  __shared__ uint32_t s_bstart[kBuckets];
-  __shared__ uint32_t s_bfill[kBuckets];
+  __shared__ __align__(16) uint64_t s_keys[kUnionMax];  // bucket scatter / sort / exact-path table / chain scratch
+  __shared__ __align__(16) uint64_t s_top[kMaxM];       // sorted top-M keys (sort and exact paths)
+  __shared__ __align__(16) uint32_t s_ids[kChainLd];
+  __shared__ __align__(16) float s_pr[kChainLd];
+  __shared__ __align__(16) float s_hit[16];
+  __shared__ __align__(16) uint32_t s_bcount[kBuckets + 64];  // + one dummy slot per lane
+  __shared__ __align__(16) uint32_t s_bstart_all[kWavesPerBlock][kBuckets];  // one copy per wavefront
   __shared__ TailShared ts;
+  __shared__ LibmTables s_tab;
+  static_assert(sizeof(uint32_t) * kChainLd * 3 + sizeof(uint64_t) * kChainLd <= sizeof(s_keys),
+                "chain scratch fits the key area");
 
-  const uint32_t tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t row = p.rpx ? grouped_index(blockIdx.x, p.rpx) : blockIdx.x;
   if (row >= p.B) return;
+
+  // 1. every global read of the row, issued before anything waits: the
+  // config, the wavefront thresholds, the candidate slots (two per 16-byte
+  // load) with the count of the wavefront that wrote them, the chain's per-row
+  // state and the libm tables (into LDS)
   const oxs_sampling_config c = p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
+  const uint32_t W = p.S * kWavesPerBlock;
+  const uint32_t span = W * p.cap_w;  // even: cap_w >= 16
+  uint64_t wt = 0;
+  if (tid < W) wt = p.wave_theta[(size_t)row * W + tid];
+  uint64_t lk[kPer];
+  uint32_t lc[kPer / 2];
+  const ulonglong2* lrow = (const ulonglong2*)(p.lists + (size_t)row * span);
+  const uint32_t* wcrow = p.wave_count + (size_t)row * W;
+#pragma unroll
+  for (int q = 0; q < kPer / 2; ++q) {  // unconditional loads (clamped index): no branches between them
+    const uint32_t pair = tid + q * kThreads;
+    const uint32_t at = 2u * pair < span ? pair : 0u;
+    const ulonglong2 k2 = lrow[at];
+    lk[2 * q] = k2.x;
+    lk[2 * q + 1] = k2.y;
+    lc[q] = wcrow[(2u * at) >> p.cap_shift];
+  }
+  RowState rs;
+  rs.uniform = p.uniforms ? p.uniforms[row] : 0.0f;
+  rs.mu = p.mu ? p.mu[row] : 0.0f;
+  rs.rng = p.rng_state ? p.rng_state[row] : 0ull;
+  rs.history_len = p.history_len ? p.history_len[row] : 0u;
+  load_libm_tables(s_tab);
+  for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
+
   const RowXf r = make_row_xf(p, c, row);
   const uint32_t M = max(c.top_k, 256u);
   if (r.dry || M > (uint32_t)kMaxM) {  // stages this build does not run on the device
@@ -1087,73 +1255,156 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     return;
   }
 
-  // 1. every wavefront's count and threshold, and all key slots at once
-  const uint32_t W = p.S * kWavesPerBlock;
-  const uint32_t span = W * p.cap_w;
-  uint32_t wc = 0;
-  uint64_t wt = 0;
-  if (tid < W) {
-    wc = p.wave_count[(size_t)row * W + tid];
-    wt = p.wave_theta[(size_t)row * W + tid];
-  }
-  constexpr int kPer = kUnionMax / kThreads;
-  uint64_t lk[kPer];
-  const uint64_t* lrow = p.lists + (size_t)row * span;
+  // 2. the largest wavefront threshold, and the largest and smallest valid key
+  uint64_t kmx = 0, kmn = ~0ull;
+  uint32_t valid = 0;
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
-    const uint32_t i = tid + q * kThreads;
-    lk[q] = i < span ? lrow[i] : 0ull;
-  }
-  const uint64_t theta_max = block_reduce_u64<true>(wt, ts.red_scratch);
-  if (tid < W) ts.wcnt[tid] = wc;
-  __syncthreads();
-
-  // 2. keep the keys at or above the largest threshold
-  uint32_t mine = 0, keepm = 0;
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const uint32_t i = tid + q * kThreads;
-    bool k = false;
-    if (i < span) {
-      const uint32_t w = i >> p.cap_shift, j = i & (p.cap_w - 1u);
-      k = j < ts.wcnt[w] && lk[q] >= theta_max && lk[q] != 0ull;
+    const uint32_t slot = 2u * (tid + (q / 2) * kThreads) + (q & 1);
+    const uint64_t k = lk[q];
+    if (slot < span && (slot & (p.cap_w - 1u)) < lc[q / 2] && k != 0ull) {
+      valid |= 1u << q;
+      kmx = k > kmx ? k : kmx;
+      kmn = k < kmn ? k : kmn;
     }
-    keepm |= (k ? 1u : 0u) << q;
-    mine += k ? 1u : 0u;
   }
-  uint32_t N;
-  uint32_t off = block_excl_scan(mine, &N, ts.scan_scratch);
-  uint64_t* U = smem_u;
+  {
+    const uint64_t a = wave_max_u64(wt), b = wave_max_u64(kmx), d = wave_min_u64(kmn);
+    if (lane == 0) {
+      ts.a_theta[wave] = a;
+      ts.a_kmax[wave] = b;
+      ts.a_kmin[wave] = d;
+    }
+  }
+  __syncthreads();
+  uint64_t theta_max = ts.a_theta[0], kmax = ts.a_kmax[0], kmin = ts.a_kmin[0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) {
+    theta_max = ts.a_theta[w] > theta_max ? ts.a_theta[w] : theta_max;
+    kmax = ts.a_kmax[w] > kmax ? ts.a_kmax[w] : kmax;
+    kmin = ts.a_kmin[w] < kmin ? ts.a_kmin[w] : kmin;
+  }
+  // keys at or above theta_max; with theta_max == kAllValid that is every valid key
+  uint32_t vm = 0;
 #pragma unroll
   for (int q = 0; q < kPer; ++q)
-    if ((keepm >> q) & 1u) U[off++] = lk[q];
-  __syncthreads();
+    if (((valid >> q) & 1u) && lk[q] >= theta_max) vm |= 1u << q;
 
   // 3. N >= M keys at or above every wavefront threshold contain the row's
   // top M; theta_max == kAllValid means every wavefront kept every candidate.
-  uint32_t meff;
-  if (N >= M || theta_max == kAllValid) {
+  // Keys are bucketed linearly in value between the largest key and a lower
+  // bound of the kept ones (the threshold itself, or the smallest key when
+  // all were kept): rounded subtraction and scaling are monotone, so bucket
+  // order agrees with key order, and only the buckets up to the one holding
+  // the M-th key are ranked, each key against the members of its bucket.
+  const bool all_kept = theta_max == kAllValid;
+  const float vmax = key_value(kmax);
+  const float vmin = all_kept ? key_value(kmin) : key_value(theta_max);
+  const float range = vmax - vmin;
+  const float scale = (float)(kBuckets - 1) / range;
+  const bool linear = kmax >= theta_max && range > 0.0f && range <= __FLT_MAX__ &&
+                      scale <= __FLT_MAX__ && vmax <= __FLT_MAX__ && vmin >= -__FLT_MAX__;
+  uint32_t meff = 0;
+  int path = 0;  // 0 buckets, 1 sort, 2 exact re-scan
+  uint32_t bs[kPer];
+  uint32_t* s_bstart = s_bstart_all[wave];
+  uint32_t last = 0;
+  if (linear) {
+    // histogram; the returned count is the key's slot inside its bucket. Every
+    // slot issues its atomic (invalid ones add 0 to this lane's dummy counter)
+    // so that the atomics go out back to back.
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const bool on = (vm >> q) & 1u;
+      const uint32_t b = on ? bucket_of(lk[q], vmax, scale) : (uint32_t)kBuckets + lane;
+      bs[q] = b | (atomicAdd(&s_bcount[b], on ? 1u : 0u) << 16);  // bucket | slot inside the bucket
+    }
+    __syncthreads();
+    // bucket starts, the count N and the bucket of the M-th key, computed by
+    // every wavefront (lane l owns buckets 4l .. 4l+3) into its own copy
+    const uint4 c4 = *(const uint4*)&s_bcount[lane * 4];
+    const uint32_t loc = c4.x + c4.y + c4.z + c4.w;
+    const uint32_t incl = wave_incl_scan(loc);
+    const uint32_t N = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    const uint32_t big = wave_max_u32(max(max(c4.x, c4.y), max(c4.z, c4.w)));
     meff = min(M, N);
+    const uint32_t st0 = incl - loc, st1 = st0 + c4.x, st2 = st1 + c4.y, st3 = st2 + c4.z;
+    *(uint4*)&s_bstart[lane * 4] = make_uint4(st0, st1, st2, st3);
+    uint32_t mine = kBuckets;
+    if (st0 < meff && st0 + c4.x >= meff) mine = lane * 4;
+    if (st1 < meff && st1 + c4.y >= meff) mine = lane * 4 + 1;
+    if (st2 < meff && st2 + c4.z >= meff) mine = lane * 4 + 2;
+    if (st3 < meff && st3 + c4.w >= meff) mine = lane * 4 + 3;
+    last = wave_reduce32(mine, MinOp{});  // the bucket of the meff-th key
+    if (N < M && !all_kept) path = 2;
+    else if (big > kBigBucket) path = 1;
+    wave_sync();
+  } else {
+    path = (theta_max == ~0ull || (!all_kept && kmax < theta_max)) ? 2 : 1;
+  }
+
+  if (path == 0) {
     if (meff == 0) {  // every logit -inf or NaN (:267-270)
       write_row_result(p, row, 0u, OXS_ROW_EMPTY);
       return;
     }
-    select_sorted(U, N, meff, smem_k, smem_t, s_bstart, s_bfill, ts);
-  } else {
-    meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)smem_u, s_bfill, smem_k, ts);
+    const uint32_t span_k = s_bstart[last] + s_bcount[last];  // keys in buckets 0 .. last
+    uint32_t start[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) start[q] = s_bstart[min(bs[q] & 0xffffu, (uint32_t)kBuckets - 1)];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      if (((vm >> q) & 1u) && (bs[q] & 0xffffu) <= last) s_keys[start[q] + (bs[q] >> 16)] = lk[q];
+    }
+    __syncthreads();
+    // rank inside the bucket; the softmax numerators (:286-290) in the same pass
+    for (uint32_t i = tid; i < span_k; i += kThreads) {
+      const uint64_t k = s_keys[i];
+      const uint32_t b = bucket_of(k, vmax, scale);
+      const uint32_t lo = s_bstart[b], hi = lo + s_bcount[b];
+      uint32_t rank = lo;
+      for (uint32_t j = lo; j < hi; ++j) rank += s_keys[j] > k ? 1u : 0u;
+      if (rank < meff) {
+        s_ids[rank] = ~(uint32_t)k;
+        s_pr[rank] = dexpf(key_value(k) - vmax, s_tab);
+      }
+    }
+    __syncthreads();
+  } else if (path == 1) {
+    const uint32_t N = sort_select(lk, vm, M, s_keys, s_top, ts);
+    if (N < M && !all_kept) {
+      path = 2;
+    } else {
+      meff = min(M, N);
+      if (meff == 0) {
+        write_row_result(p, row, 0u, OXS_ROW_EMPTY);
+        return;
+      }
+      keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
+    }
+  }
+  if (path == 2) {
+    meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)s_keys, s_bcount, s_top, ts);
     if (meff == 0) {
       write_row_result(p, row, 0u, OXS_ROW_EMPTY);
       return;
     }
-    bitonic_sort<false>(smem_k, meff);
+    bitonic_sort<false>(s_top, meff);
+    keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
   }
 
-  // 4. the chain after the top-M selection
-  uint32_t* ids = (uint32_t*)smem_u;
-  float* pr = (float*)(ids + kMaxM);
-  uint32_t* ids2 = (uint32_t*)(pr + kMaxM);
-  float* pr2 = (float*)(ids2 + kMaxM);
-  tail_chain(p, c, row, smem_k, meff, ids, pr, ids2, pr2, smem_t, ts);
+  // 4. the chain after the top-M selection, in the first wavefront
+  if (wave != 0) return;
+  uint32_t* scratch = (uint32_t*)s_keys;
+  ChainBufs bf;
+  bf.ids = s_ids;
+  bf.pr = s_pr;
+  bf.ids_b = scratch;
+  bf.pr_b = (float*)(scratch + kChainLd);
+  bf.aux = (float*)(scratch + 2 * kChainLd);
+  bf.aux64 = (uint64_t*)(scratch + 3 * kChainLd);
+  bf.hit = s_hit;
+  wave_chain(p, c, row, meff, bf, rs, s_tab);
 }
 
 // ---------------------------------------------------------------- host side
