@@ -41,13 +41,13 @@ namespace oxs {
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / 64;
-constexpr int kUnionMax = 4096;   // candidate keys per row (tail LDS)
+constexpr int kUnionMax = 2048;   // candidate key slots per row
+constexpr int kTailArea = 4096;   // 64-bit words of tail LDS shared by the scatter, sort, exact-path table and chain scratch
 constexpr int kMaxM = 1024;       // largest max(top_k, 256) run on the device
 constexpr int kMaxChunk = 8192;   // logits per stream block
 constexpr int kMaxChunks = 64;    // chunks per row
-constexpr int kHashSlots = 256;   // marked (sparse-stage) ids per stream block
 constexpr int kBuckets = 256;     // tail counting-sort buckets
-constexpr int kHistUnroll = 4;    // history ids per thread loaded ahead of the stream
+constexpr int kHistUnroll = 4;    // history-window ids per stream thread read with the logits
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -55,7 +55,6 @@ constexpr uint32_t kCountMask = 0x0fffffffu;
 constexpr uint32_t kBanFlag = 1u << 28;
 constexpr uint32_t kBiasFlag = 1u << 29;
 constexpr uint32_t kNlFlag = 1u << 30;
-constexpr uint32_t kEmpty = 0xffffffffu;
 
 struct Params {
   const void* logits;
@@ -93,6 +92,7 @@ struct Params {
   uint64_t* lists;       // [B][S*4][cap_w]
   uint64_t* wave_theta;  // [B][S*4]
   uint32_t* wave_count;  // [B][S*4]
+  const uint64_t* libm;  // [kLibmWords]: the libm tables (exp2, 1/c, ln c, log2 c) as bit patterns
 };
 
 // ---------------------------------------------------------------- keys
@@ -126,6 +126,15 @@ __device__ __forceinline__ uint32_t grouped_index(uint32_t block, uint32_t per_x
 
 // ---------------------------------------------------------------- row setup
 
+// p[i], or dflt when p is null, read without a branch (from an in-bounds dummy
+// address when p is null): loads inside branches make the compiler wait for
+// every outstanding load at the branch's end.
+template <typename T>
+__device__ __forceinline__ T load_or(const T* ptr, size_t i, T dflt, const void* dummy) {
+  const T v = ptr ? ptr[i] : *(const T*)dummy;
+  return ptr ? v : dflt;
+}
+
 // Per-row constants of the pre-softmax stages (sampler.rs:184-254).
 struct RowXf {
   bool pen_rep, pen_fp, use_hist, nl_active, any_special, do_temp, dry;
@@ -134,10 +143,10 @@ struct RowXf {
   uint32_t bias_off, bias_cnt, ban_off, ban_cnt;
 };
 
-__device__ __forceinline__ RowXf make_row_xf(const Params& p, const oxs_sampling_config& c,
-                                             uint32_t row) {
+__device__ __forceinline__ RowXf make_row_xf_h(const Params& p, const oxs_sampling_config& c,
+                                               uint32_t hlen) {
   RowXf r;
-  uint32_t hlen = (p.history && p.history_len) ? p.history_len[row] : 0u;
+  if (!(p.history && p.history_len)) hlen = 0u;
   if ((int64_t)hlen > p.history_ld) hlen = (uint32_t)p.history_ld;
   r.hlen = hlen;
   r.rp = c.repeat_penalty;
@@ -163,9 +172,31 @@ __device__ __forceinline__ RowXf make_row_xf(const Params& p, const oxs_sampling
   return r;
 }
 
+__device__ __forceinline__ RowXf make_row_xf(const Params& p, const oxs_sampling_config& c,
+                                             uint32_t row) {
+  return make_row_xf_h(p, c, load_or<uint32_t>(p.history_len, row, 0u, p.configs));
+}
+
 // The sparse pre-softmax stages for one marked logit, in reference order:
 // ban (:184-188), bias (:189-193), newline (:196-200), repetition (:217-229),
 // frequency/presence (:232-245). Temperature is applied by the caller.
+// The same stages with the id's bias value already found.
+__device__ __forceinline__ float apply_special_b(const RowXf& r, float x, uint32_t entry, float bias) {
+  if (entry & kBanFlag) x = neg_inf();
+  if (entry & kBiasFlag) x += bias;
+  if (entry & kNlFlag) x -= r.nl_pen;
+  const uint32_t cnt = entry & kCountMask;
+  if (cnt) {
+    if (r.pen_rep) x = (x > 0.0f) ? x / r.rp : x * r.rp;
+    if (r.pen_fp) {
+      const float t = (float)cnt * r.fp;
+      const float pen = t + r.pp;
+      x = x - pen;
+    }
+  }
+  return x;
+}
+
 __device__ __forceinline__ float apply_special(const uint32_t* bias_ids, const float* bias_values,
                                                const RowXf& r, float x, uint32_t entry,
                                                uint32_t idx) {
@@ -299,19 +330,22 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scrat
   return x - v + before;
 }
 
-// ---------------------------------------------------------------- marked-id hash (LDS)
+// ---------------------------------------------------------------- marked ids (stream LDS hash)
 
+// A stream block marks the sparse-stage ids of its chunk (history window
+// with counts, bans, biases, newline) in an LDS bitmap and an open-addressing
+// hash keyed by chunk offset.
+constexpr int kHashSlots = 256;
+constexpr uint32_t kEmptySlot = 0xffffffffu;
 __device__ __forceinline__ uint32_t hash_slot(uint32_t key) { return (key * 0x9e3779b1u) >> 24; }
 static_assert(kHashSlots == 256, "hash_slot yields 8 bits");
 
-// Inserts `key` (a chunk-local offset), adding `add` and OR-ing `orv` into its
-// value; false when the table is full.
-__device__ bool hash_insert(uint32_t* hkeys, uint32_t* hvals, uint32_t key, uint32_t add,
-                            uint32_t orv) {
+// Continues an insertion whose home slot held another key; false when full.
+__device__ bool hash_insert_from(uint32_t* hkeys, uint32_t* hvals, uint32_t key, uint32_t add, uint32_t orv) {
   uint32_t h = hash_slot(key);
   for (int probe = 0; probe < kHashSlots; ++probe) {
-    const uint32_t prev = atomicCAS(&hkeys[h], kEmpty, key);
-    if (prev == kEmpty || prev == key) {
+    const uint32_t prev = atomicCAS(&hkeys[h], kEmptySlot, key);
+    if (prev == kEmptySlot || prev == key) {
       if (add) atomicAdd(&hvals[h], add);
       if (orv) atomicOr(&hvals[h], orv);
       return true;
@@ -321,22 +355,22 @@ __device__ bool hash_insert(uint32_t* hkeys, uint32_t* hvals, uint32_t key, uint
   return false;
 }
 
-__device__ __forceinline__ int hash_find(const uint32_t* hkeys, uint32_t key) {
+__device__ __forceinline__ uint32_t hash_lookup(const uint32_t* hkeys, const uint32_t* hvals, uint32_t key) {
   uint32_t h = hash_slot(key);
   for (int probe = 0; probe < kHashSlots; ++probe) {
     const uint32_t k = hkeys[h];
-    if (k == key) return (int)h;
-    if (k == kEmpty) return -1;
+    if (k == key) return hvals[h];
+    if (k == kEmptySlot) return 0u;
     h = (h + 1) & (kHashSlots - 1);
   }
-  return -1;
+  return 0u;
 }
 
-// Marks one chunk-local id.
-__device__ __forceinline__ bool mark(uint32_t* bitmap, uint32_t* hkeys, uint32_t* hvals,
-                                     uint32_t off, uint32_t add, uint32_t orv) {
+// Marks one chunk offset: bitmap bit, then the hash entry.
+__device__ __forceinline__ bool mark_off(uint32_t* bitmap, uint32_t* hkeys, uint32_t* hvals, uint32_t off,
+                                         uint32_t add, uint32_t orv) {
   atomicOr(&bitmap[off >> 5], 1u << (off & 31));
-  return hash_insert(hkeys, hvals, off, add, orv);
+  return hash_insert_from(hkeys, hvals, off, add, orv);
 }
 
 // ---------------------------------------------------------------- stream kernel
@@ -344,6 +378,206 @@ __device__ __forceinline__ bool mark(uint32_t* bitmap, uint32_t* hkeys, uint32_t
 constexpr uint32_t kMinValidOrd = 0x00800000u;  // f2ord(-FLT_MAX): every candidate key is >= this
 constexpr uint64_t kAllValid = (uint64_t)kMinValidOrd << 32;  // threshold of a wavefront that kept all
 
+// The (row, chunk) of a stream block. With rpx > 0 the hardware's round-robin
+// placement of blocks on the 8 XCDs (block i on XCD i % 8) gives XCD x the
+// chunks of rows [x * rpx, (x + 1) * rpx), so that a row's stream blocks and
+// its tail block share one L2.
+__device__ __forceinline__ void unit_of(const Params& p, uint32_t* row, uint32_t* chunk) {
+  const uint32_t k = p.rpx ? grouped_index(blockIdx.x, p.rpx * p.S) : blockIdx.x;
+  *row = k / p.S;
+  *chunk = k - *row * p.S;
+}
+
+__device__ __forceinline__ const oxs_sampling_config& row_config(const Params& p, uint32_t row) {
+  return p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
+}
+
+// One unit after its logits arrived. Dense stages (grammar mask, end of
+// vocabulary) in registers; the masked raw logits are staged in each thread's
+// own LDS slots. The logits whose sparse stages apply (history window, bans,
+// biases, newline) are marked in the chunk's LDS bitmap and hash and get their
+// exact values from the thread that holds them. Each wavefront finds a lower
+// bound of the c_w-th largest of its 64 lane maxima over the masked raw logits
+// and emits every logit at or above it as
+// (order key of x / temperature << 32 | ~token id); the threshold it reports
+// is in the same scaled values.
+template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
+__device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint32_t chunk, const RowXf& r,
+                                             const uint32_t (&raw)[SLOTS][(DT == OXS_DTYPE_F32) ? 4 : 8],
+                                             const uint32_t (&mw)[SLOTS], const uint32_t (&hv)[kHistUnroll],
+                                             float* s_x, uint32_t* s_bitmap, uint32_t* s_hkeys,
+                                             uint32_t* s_hvals, uint32_t* s_full) {
+  constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;
+  constexpr int TILE = kThreads * EPL;
+  constexpr int NE = SLOTS * EPL;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t CH = SLOTS * TILE;
+  const uint32_t c0 = chunk * CH;
+  const uint32_t c1 = min(c0 + CH, p.V);
+  const float inv_t = r.do_temp ? r.inv_temp : 1.0f;
+  // Survivors are found on the masked raw logits when the temperature scale
+  // is a finite positive number (x -> x * inv_t is then monotone); only
+  // survivors are scaled. Otherwise they are found on the scaled values.
+  const bool wy = WB || inv_t == 1.0f || !(inv_t > 0.0f && inv_t <= __FLT_MAX__);
+  auto wval = [=](float x) { return wy ? x * inv_t : x; };
+
+  // ---- masked raw logits, staged in this thread's LDS slots; lane maximum
+  float v[NE];
+  float lmax = neg_inf();
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const uint32_t off = s * TILE + tid * EPL;  // chunk-local
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float x = __uint_as_float(raw[s][e]);
+      if (MASK && !((mw[s] >> ((c0 + off + e) & 31)) & 1u)) x = neg_inf();
+      if (!VEC && c0 + off + e >= c1) x = neg_inf();
+      if (VEC && c0 + off >= c1) x = neg_inf();  // past the end of a short last chunk
+      v[s * EPL + e] = x;
+      lmax = fmaxf(lmax, wval(x));  // a NaN here only lowers the pruning, never correctness
+      if (WB && c0 + off + e < c1) p.logits_out[(size_t)row * p.logits_out_ld + c0 + off + e] = x * inv_t;
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4)
+      *(float4*)&s_x[(s * kThreads + tid) * EPL + e] =
+          make_float4(v[s * EPL + e], v[s * EPL + e + 1], v[s * EPL + e + 2], v[s * EPL + e + 3]);
+  }
+
+  // ---- sparse-stage ids of this chunk: bitmap and hash (a count per history
+  // window occurrence, a flag per ban, bias, newline); the first claim of
+  // every window id's home slot goes out at once, collisions after
+  uint32_t umask = 0;
+  if (r.any_special) {
+    bool ok = true;
+    uint32_t prev[kHistUnroll];
+#pragma unroll
+    for (int q = 0; q < kHistUnroll; ++q) {
+      const uint32_t t = r.use_hist && tid + q * kThreads < r.wn ? hv[q] : 0xffffffffu;
+      const bool in = t >= c0 && t < c1;
+      prev[q] = in ? atomicCAS(&s_hkeys[hash_slot(t - c0)], kEmptySlot, t - c0) : 0u;
+      if (in) atomicOr(&s_bitmap[(t - c0) >> 5], 1u << ((t - c0) & 31));
+    }
+#pragma unroll
+    for (int q = 0; q < kHistUnroll; ++q) {
+      const uint32_t t = r.use_hist && tid + q * kThreads < r.wn ? hv[q] : 0xffffffffu;
+      if (!(t >= c0 && t < c1)) continue;
+      if (prev[q] == kEmptySlot || prev[q] == t - c0) atomicAdd(&s_hvals[hash_slot(t - c0)], 1u);
+      else ok &= hash_insert_from(s_hkeys, s_hvals, t - c0, 1u, 0u);
+    }
+    if (r.use_hist) {
+      const uint32_t* hrow = p.history + (size_t)row * p.history_ld + r.wstart;
+      for (uint32_t j = tid + kHistUnroll * kThreads; j < r.wn; j += kThreads) {  // long windows
+        const uint32_t t = hrow[j];
+        if (t >= c0 && t < c1) ok &= mark_off(s_bitmap, s_hkeys, s_hvals, t - c0, 1u, 0u);
+      }
+    }
+    for (uint32_t k = tid; k < r.ban_cnt; k += kThreads) {
+      const uint32_t id = p.ban_ids[r.ban_off + k];
+      if (id >= c0 && id < c1) ok &= mark_off(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBanFlag);
+    }
+    for (uint32_t k = tid; k < r.bias_cnt; k += kThreads) {
+      const uint32_t id = p.bias_ids[r.bias_off + k];
+      if (id >= c0 && id < c1) ok &= mark_off(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBiasFlag);
+    }
+    if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1)
+      ok &= mark_off(s_bitmap, s_hkeys, s_hvals, r.nl_id - c0, 0u, kNlFlag);
+    if (!ok) *s_full = 1;
+    __syncthreads();  // marks complete
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      const uint32_t off = s * TILE + tid * EPL;
+      umask |= ((s_bitmap[off >> 5] >> (off & 31)) & ((1u << EPL) - 1u)) << (s * EPL);
+    }
+  }
+
+  // ---- wavefront threshold: a lower bound of the c_w-th largest lane
+  // maximum, from the top 16 bits of the order keys
+  const uint32_t lm = f2ord(lmax);
+  uint32_t theta = 0;
+#pragma unroll
+  for (int bit = 31; bit >= 16; --bit) {
+    const uint32_t trial = theta | (1u << bit);
+    if ((uint32_t)__popcll(__ballot(lm >= trial)) >= p.c_w) theta = trial;
+  }
+  float theta_f;
+  uint32_t th_ord;  // every candidate of this wavefront whose scaled order key is >= th_ord is emitted
+  if (theta < kMinValidOrd) {  // too few candidates: keep every one
+    theta = kMinValidOrd;
+    theta_f = -__FLT_MAX__;
+    th_ord = kMinValidOrd;
+  } else {
+    theta_f = ord2f(theta);
+    // unemitted logits are < theta_f, so their scaled values are <= theta_f * inv_t
+    th_ord = wy ? theta : f2ord(theta_f * inv_t) + 1u;
+  }
+  uint32_t smask = 0;  // bit i: wval(x_i) >= theta_f (false for -inf and NaN), unmarked
+#pragma unroll
+  for (int i = 0; i < NE; ++i) smask |= (wval(v[i]) >= theta_f ? 1u : 0u) << i;
+  smask &= ~umask;
+
+  // ---- survivors into this wavefront's list; slots from the wavefront's
+  // ballot of the lanes that emit, in lane order
+  const size_t wslot = ((size_t)row * p.S + chunk) * kWavesPerBlock + wave;
+  uint64_t* out = p.lists + wslot * p.cap_w;
+  uint32_t base = 0;
+  while (true) {
+    if (__ballot(smask != 0u) == 0) break;
+    bool want = false;
+    uint64_t key = 0;
+    if (smask) {
+      const uint32_t b = __builtin_ctz(smask);
+      smask &= smask - 1u;
+      const uint32_t sl = b / EPL, e = b % EPL;
+      const float y = s_x[(sl * kThreads + tid) * EPL + e] * inv_t;
+      const uint32_t k = cand_key(y);
+      want = k != 0u;
+      key = comp_key(k, c0 + sl * TILE + tid * EPL + e);
+    }
+    const uint64_t m = __ballot(want);
+    if (want) {
+      const uint32_t q = base + lanes_below(m);
+      if (q < p.cap_w) out[q] = key;
+    }
+    base += (uint32_t)__popcll(m);
+  }
+
+  // ---- this thread's marked logits at their exact values (sampler.rs:184-254)
+  if (r.any_special) {
+    while (true) {
+      if (__ballot(umask != 0u) == 0) break;
+      bool want = false;
+      uint64_t key = 0;
+      if (umask) {
+        const uint32_t b = __builtin_ctz(umask);
+        umask &= umask - 1u;
+        const uint32_t sl = b / EPL, e = b % EPL;
+        const uint32_t off = sl * TILE + tid * EPL + e;
+        float y = apply_special(p.bias_ids, p.bias_values, r, s_x[(sl * kThreads + tid) * EPL + e],
+                                hash_lookup(s_hkeys, s_hvals, off), c0 + off);
+        y *= inv_t;
+        if (WB && c0 + off < c1) p.logits_out[(size_t)row * p.logits_out_ld + c0 + off] = y;
+        const uint32_t k = cand_key(y);
+        want = k != 0u && k >= th_ord;
+        key = comp_key(k, c0 + off);
+      }
+      const uint64_t m = __ballot(want);
+      if (want) {
+        const uint32_t q = base + lanes_below(m);
+        if (q < p.cap_w) out[q] = key;
+      }
+      base += (uint32_t)__popcll(m);
+    }
+  }
+  if (lane == 0) {
+    const bool bad = base > p.cap_w || (r.any_special && *s_full != 0u);
+    p.wave_theta[wslot] = bad ? ~0ull : ((uint64_t)th_ord << 32);
+    p.wave_count[wslot] = bad ? 0u : base;
+  }
+}
+
+// One (row, chunk) per block: the row's history length and config first,
+// the chunk's logits and mask words, then the history window ids (the
+// sparse-stage marks need them only after the logits are in).
 template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
 __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
   constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;  // logits per 16-byte load
@@ -354,34 +588,21 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
   static_assert(CH <= kMaxChunk, "chunk too large");
   static_assert(NE <= 32, "one survivor bit per logit of a lane");
 
-  __shared__ __align__(16) float s_x[CH];  // the chunk's masked raw logits
-  __shared__ uint32_t s_bitmap[CH / 32];  // marked (sparse-stage) ids
+  __shared__ __align__(16) float s_x[NE * kThreads];  // each thread's masked raw logits (private slots)
+  __shared__ uint32_t s_bitmap[CH / 32];              // marked (sparse-stage) ids of the chunk
   __shared__ uint32_t s_hkeys[kHashSlots];
   __shared__ uint32_t s_hvals[kHashSlots];
-  __shared__ uint32_t s_wcount[kWavesPerBlock];
-  __shared__ uint32_t s_wover[kWavesPerBlock];
-  __shared__ uint32_t s_wtheta[kWavesPerBlock];
   __shared__ uint32_t s_full;
 
   const uint32_t tid = threadIdx.x;
-  const uint32_t lane = tid & 63;
-  const uint32_t wave = tid >> 6;
   uint32_t row, chunk;
-  if (p.rpx) {
-    const uint32_t v = grouped_index(blockIdx.x, p.rpx * p.S);
-    row = v / p.S;
-    chunk = v - row * p.S;
-  } else {
-    row = blockIdx.x / p.S;
-    chunk = blockIdx.x - row * p.S;
-  }
+  unit_of(p, &row, &chunk);
   if (row >= p.B) return;
-  const oxs_sampling_config c = p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
-  const RowXf r = make_row_xf(p, c, row);
   const uint32_t c0 = chunk * CH;
   const uint32_t c1 = min(c0 + (uint32_t)CH, p.V);
+  const RowXf r = make_row_xf(p, row_config(p, row), row);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- 1. the chunk's logits and mask words, then the history window ids
   uint32_t raw[SLOTS][EPL];
   const char* rowp = (const char*)p.logits + (size_t)row * (size_t)p.ld * ESZ;
 #pragma unroll
@@ -389,7 +610,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
     const uint32_t base = c0 + s * TILE + tid * EPL;
     if constexpr (VEC) {
       // V is a multiple of EPL here: past-the-end groups re-read the row's
-      // last group (in bounds) and their values are dropped below.
+      // last group (in bounds) and their values are dropped later.
       const uint32_t at = base < c1 ? base : p.V - EPL;
       const u32x4 q = __builtin_nontemporal_load((const u32x4*)(rowp + (size_t)at * ESZ));
       if constexpr (DT == OXS_DTYPE_F32) {
@@ -411,155 +632,35 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
   uint32_t mw[SLOTS];
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s) {
+    mw[s] = 0xffffffffu;
     if constexpr (MASK) {
-      const uint32_t base = c0 + s * TILE + tid * EPL;
-      const uint32_t at = base < c1 ? base : p.V - 1;
-      mw[s] = p.mask[(size_t)row * p.mask_ld + (at >> 5)];
-    } else {
-      mw[s] = 0xffffffffu;
+      const uint32_t b2 = c0 + s * TILE + tid * EPL;
+      mw[s] = p.mask[(size_t)row * p.mask_ld + ((b2 < c1 ? b2 : p.V - 1) >> 5)];
     }
   }
+  // history window ids, read without a branch (an in-bounds dummy address
+  // where the row has none): unconditional reads keep the waits on the
+  // logits exact
   uint32_t hv[kHistUnroll];
-  const uint32_t* hrow = p.history + (size_t)row * p.history_ld + r.wstart;
+  const uint32_t* hsrc = r.use_hist ? p.history + (size_t)row * p.history_ld + r.wstart : (const uint32_t*)p.configs;
+  const uint32_t hn = r.use_hist ? r.wn : 0u;
 #pragma unroll
   for (int q = 0; q < kHistUnroll; ++q) {
     const uint32_t j = tid + q * kThreads;
-    hv[q] = (r.use_hist && j < r.wn) ? hrow[j] : kEmpty;
+    hv[q] = hsrc[j < hn ? j : 0u];
   }
-
-  if (lane == 0) {
-    s_wcount[wave] = 0;
-    s_wover[wave] = 0;
-  }
-  if (r.any_special) {
+  if (r.any_special) {  // tables cleared while the reads are in flight
     for (uint32_t i = tid; i < (uint32_t)CH / 32; i += kThreads) s_bitmap[i] = 0;
     for (uint32_t i = tid; i < (uint32_t)kHashSlots; i += kThreads) {
-      s_hkeys[i] = kEmpty;
+      s_hkeys[i] = kEmptySlot;
       s_hvals[i] = 0;
     }
     if (tid == 0) s_full = 0;
-  }
-
-  // ---- 2. dense stages in registers; the masked raw logits are kept in LDS
-  const float inv_t = r.do_temp ? r.inv_temp : 1.0f;  // x * 1.0f is exact
-  float x[NE];
-  float lmax = neg_inf();
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    const uint32_t off = s * TILE + tid * EPL;  // chunk-local
-    float v[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      v[e] = __uint_as_float(raw[s][e]);
-      if (MASK && !((mw[s] >> ((c0 + off + e) & 31)) & 1u)) v[e] = neg_inf();
-    }
-    if (c0 + off >= c1) {  // past the end of a short last chunk
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) v[e] = neg_inf();
-    }
-#pragma unroll
-    for (int e = 0; e < EPL; e += 4) *(float4*)&s_x[off + e] = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const float y = v[e] * inv_t;
-      x[s * EPL + e] = y;
-      lmax = fmaxf(lmax, y);  // a NaN here only lowers the pruning, never correctness
-      if (WB && c0 + off + e < c1) p.logits_out[(size_t)row * p.logits_out_ld + c0 + off + e] = y;
-    }
-  }
-
-  // ---- 3. wavefront threshold: a lower bound of the c_w-th largest lane
-  // maximum, from the top 16 bits of the order keys
-  const uint32_t lm = f2ord(lmax);
-  uint32_t theta = 0;
-#pragma unroll 1
-  for (int bit = 31; bit >= 16; --bit) {
-    const uint32_t trial = theta | (1u << bit);
-    if ((uint32_t)__popcll(__ballot(lm >= trial)) >= p.c_w) theta = trial;
-  }
-  float theta_f;
-  if (theta < kMinValidOrd) {  // too few candidates: keep every one
-    theta = kMinValidOrd;
-    theta_f = -__FLT_MAX__;
-  } else {
-    theta_f = ord2f(theta);
-  }
-  uint32_t smask = 0;  // bit i: x[i] >= theta_f (false for -inf and NaN)
-#pragma unroll
-  for (int i = 0; i < NE; ++i) smask |= (x[i] >= theta_f ? 1u : 0u) << i;
-
-  // ---- 4. mark the chunk's sparse-stage ids (bans, biases, newline, history)
-  if (r.any_special) {
-    __syncthreads();  // LDS tables cleared
-    bool ok = true;
-#pragma unroll
-    for (int q = 0; q < kHistUnroll; ++q) {
-      const uint32_t t = hv[q];
-      if (t >= c0 && t < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, t - c0, 1u, 0u);
-    }
-    if (r.use_hist) {
-      for (uint32_t j = tid + kHistUnroll * kThreads; j < r.wn; j += kThreads) {  // long windows
-        const uint32_t t = hrow[j];
-        if (t >= c0 && t < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, t - c0, 1u, 0u);
-      }
-    }
-    for (uint32_t k = tid; k < r.ban_cnt; k += kThreads) {
-      const uint32_t id = p.ban_ids[r.ban_off + k];
-      if (id >= c0 && id < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBanFlag);
-    }
-    for (uint32_t k = tid; k < r.bias_cnt; k += kThreads) {
-      const uint32_t id = p.bias_ids[r.bias_off + k];
-      if (id >= c0 && id < c1) ok &= mark(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBiasFlag);
-    }
-    if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1)
-      ok &= mark(s_bitmap, s_hkeys, s_hvals, r.nl_id - c0, 0u, kNlFlag);
-    if (!ok) s_full = 1;
-    __syncthreads();  // marks complete
-  }
-
-  // ---- 5. survivors (unmarked, x >= theta_f) into this wavefront's list
-  const size_t wslot = ((size_t)row * p.S + chunk) * kWavesPerBlock + wave;
-  uint64_t* out = p.lists + wslot * p.cap_w;
-  while (smask) {
-    const uint32_t b = __builtin_ctz(smask);
-    smask &= smask - 1u;
-    const uint32_t off = (b / EPL) * TILE + tid * EPL + (b % EPL);
-    if (r.any_special && ((s_bitmap[off >> 5] >> (off & 31)) & 1u)) continue;
-    const float y = s_x[off] * inv_t;
-    const uint32_t q = atomicAdd(&s_wcount[wave], 1u);
-    if (q < p.cap_w) out[q] = comp_key(f2ord(y), c0 + off);
-    else s_wover[wave] = 1u;
-  }
-  if (lane == 0) s_wtheta[wave] = theta;
-
-  // ---- 6. exact values of the marked ids; those at or above the block's
-  // largest threshold join the lists (the tail drops smaller keys)
-  if (r.any_special) {
-    __syncthreads();
-    uint32_t tb = s_wtheta[0];
-#pragma unroll
-    for (int w = 1; w < kWavesPerBlock; ++w) tb = max(tb, s_wtheta[w]);
-    for (uint32_t h = tid; h < (uint32_t)kHashSlots; h += kThreads) {
-      const uint32_t off = s_hkeys[h];
-      if (off == kEmpty) continue;
-      const uint32_t idx = c0 + off;
-      float y = apply_special(p.bias_ids, p.bias_values, r, s_x[off], s_hvals[h], idx);
-      y *= inv_t;
-      if (WB) p.logits_out[(size_t)row * p.logits_out_ld + idx] = y;
-      const uint32_t k = cand_key(y);
-      if (k && k >= tb) {
-        const uint32_t q = atomicAdd(&s_wcount[wave], 1u);
-        if (q < p.cap_w) out[q] = comp_key(k, idx);
-        else s_wover[wave] = 1u;
-      }
-    }
     __syncthreads();
   }
-  if (lane == 0) {
-    const bool bad = s_wover[wave] != 0u || (r.any_special && s_full != 0u);
-    p.wave_theta[wslot] = bad ? ~0ull : ((uint64_t)theta << 32);
-    p.wave_count[wslot] = bad ? 0u : min(s_wcount[wave], p.cap_w);
-  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  process_unit<DT, SLOTS, VEC, MASK, WB>(p, row, chunk, r, raw, mw, hv, s_x, s_bitmap, s_hkeys, s_hvals, &s_full);
 }
 
 // ---------------------------------------------------------------- tail helpers
@@ -731,12 +832,24 @@ struct LibmTables {
   double log2c[16];
 };
 
-__device__ __forceinline__ void load_libm_tables(LibmTables& t) {
+// The tables come from a workspace copy (made when the sampler is created):
+// ordinary reads issued with the row's first loads; stored into LDS later.
+constexpr int kLibmWords = 32 + 16 * 3;
+struct LibmEntries {
+  uint64_t e, i, l, g;
+};
+__device__ __forceinline__ LibmEntries fetch_libm_tables(const uint64_t* w) {
   const uint32_t tid = threadIdx.x;
-  if (tid < 32) t.exp2[tid] = oxs_libm::kExp2Tab[tid];
-  else if (tid < 48) t.invc[tid - 32] = oxs_libm::kLogInvc[tid - 32];
-  else if (tid < 64) t.lnc[tid - 48] = oxs_libm::kLnLogc[tid - 48];
-  else if (tid < 80) t.log2c[tid - 64] = oxs_libm::kLog2Logc[tid - 64];
+  return LibmEntries{w[tid & 31u], w[32 + (tid & 15u)], w[48 + (tid & 15u)], w[64 + (tid & 15u)]};
+}
+__device__ __forceinline__ void store_libm_tables(const LibmEntries& v, LibmTables& t) {
+  const uint32_t tid = threadIdx.x;
+  if (tid < 32) t.exp2[tid] = v.e;
+  if (tid < 16) {
+    t.invc[tid] = __longlong_as_double((long long)v.i);
+    t.lnc[tid] = __longlong_as_double((long long)v.l);
+    t.log2c[tid] = __longlong_as_double((long long)v.g);
+  }
 }
 
 __device__ __forceinline__ float dexpf(float x, const LibmTables& t) {
@@ -1198,7 +1311,8 @@ __device__ void keys_to_chain(const uint64_t* keys, uint32_t n, uint32_t* ids, f
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
-  __shared__ __align__(16) uint64_t s_keys[kUnionMax];  // bucket scatter / sort / exact-path table / chain scratch
+  __shared__ __align__(16) uint64_t s_keys[kTailArea];  // bucket scatter / sort / exact-path table / chain scratch
+  static_assert(kTailArea >= kUnionMax && kTailArea * 2 >= kMaxChunk, "tail LDS area");
   __shared__ __align__(16) uint64_t s_top[kMaxM];       // sorted top-M keys (sort and exact paths)
   __shared__ __align__(16) uint32_t s_ids[kChainLd];
   __shared__ __align__(16) float s_pr[kChainLd];
@@ -1216,13 +1330,17 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
 
   // 1. every global read of the row, issued before anything waits: the
   // config, the wavefront thresholds, the candidate slots (two per 16-byte
-  // load) with the count of the wavefront that wrote them, the chain's per-row
-  // state and the libm tables (into LDS)
+  // load) with the count of the wavefront that wrote them, the history
+  // window, the chain's per-row state and the libm tables (into LDS)
+  // (reads whose values are needed first are issued first: a wait covers
+  // every read issued before the one it waits for)
   const oxs_sampling_config c = p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
+  const uint32_t hlen0 = load_or<uint32_t>(p.history_len, row, 0u, p.configs);
+  const LibmEntries tabv = fetch_libm_tables(p.libm);
+  const RowXf r = make_row_xf_h(p, c, hlen0);
   const uint32_t W = p.S * kWavesPerBlock;
-  const uint32_t span = W * p.cap_w;  // even: cap_w >= 16
-  uint64_t wt = 0;
-  if (tid < W) wt = p.wave_theta[(size_t)row * W + tid];
+  const uint32_t span = W * p.cap_w;  // even: cap_w >= 8
+  const uint64_t wt0 = p.wave_theta[(size_t)row * W + (tid < W ? tid : 0u)];
   uint64_t lk[kPer];
   uint32_t lc[kPer / 2];
   const ulonglong2* lrow = (const ulonglong2*)(p.lists + (size_t)row * span);
@@ -1237,14 +1355,16 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     lc[q] = wcrow[(2u * at) >> p.cap_shift];
   }
   RowState rs;
-  rs.uniform = p.uniforms ? p.uniforms[row] : 0.0f;
-  rs.mu = p.mu ? p.mu[row] : 0.0f;
-  rs.rng = p.rng_state ? p.rng_state[row] : 0ull;
-  rs.history_len = p.history_len ? p.history_len[row] : 0u;
-  load_libm_tables(s_tab);
+  rs.uniform = load_or<float>(p.uniforms, row, 0.0f, p.configs);
+  rs.mu = load_or<float>(p.mu, row, 0.0f, p.configs);
+  rs.rng = load_or<uint64_t>(p.rng_state, row, 0ull, p.configs);
+  rs.history_len = hlen0;
+  const uint64_t wt = tid < W ? wt0 : 0ull;
+  __builtin_amdgcn_sched_barrier(0);  // every read above is issued before anything waits
+  store_libm_tables(tabv, s_tab);
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
 
-  const RowXf r = make_row_xf(p, c, row);
+
   const uint32_t M = max(c.top_k, 256u);
   if (r.dry || M > (uint32_t)kMaxM) {  // stages this build does not run on the device
     write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED);
@@ -1284,39 +1404,41 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     kmax = ts.a_kmax[w] > kmax ? ts.a_kmax[w] : kmax;
     kmin = ts.a_kmin[w] < kmin ? ts.a_kmin[w] : kmin;
   }
-  // keys at or above theta_max; with theta_max == kAllValid that is every valid key
+  const bool all_kept = theta_max == kAllValid;
+  const bool exact = theta_max == ~0ull;
+  // 3. kept keys: at or above every wavefront threshold (with kAllValid,
+  // every valid key)
   uint32_t vm = 0;
+  const uint64_t (&yk)[kPer] = lk;
 #pragma unroll
   for (int q = 0; q < kPer; ++q)
     if (((valid >> q) & 1u) && lk[q] >= theta_max) vm |= 1u << q;
 
-  // 3. N >= M keys at or above every wavefront threshold contain the row's
-  // top M; theta_max == kAllValid means every wavefront kept every candidate.
-  // Keys are bucketed linearly in value between the largest key and a lower
-  // bound of the kept ones (the threshold itself, or the smallest key when
-  // all were kept): rounded subtraction and scaling are monotone, so bucket
-  // order agrees with key order, and only the buckets up to the one holding
-  // the M-th key are ranked, each key against the members of its bucket.
-  const bool all_kept = theta_max == kAllValid;
+  // 4. N >= M kept keys contain the row's top M. Keys are bucketed linearly
+  // in value between the largest key and a lower bound of the kept ones (the
+  // threshold, or the smallest key when all were kept): rounded subtraction
+  // and scaling are monotone, so bucket order agrees with key order, and only
+  // the buckets up to the one holding the M-th key are ranked, each key
+  // against the members of its bucket.
   const float vmax = key_value(kmax);
   const float vmin = all_kept ? key_value(kmin) : key_value(theta_max);
   const float range = vmax - vmin;
   const float scale = (float)(kBuckets - 1) / range;
-  const bool linear = kmax >= theta_max && range > 0.0f && range <= __FLT_MAX__ &&
+  const bool linear = !exact && kmax >= theta_max && range > 0.0f && range <= __FLT_MAX__ &&
                       scale <= __FLT_MAX__ && vmax <= __FLT_MAX__ && vmin >= -__FLT_MAX__;
   uint32_t meff = 0;
-  int path = 0;  // 0 buckets, 1 sort, 2 exact re-scan
+  int path = exact ? 2 : 1;  // 0 buckets, 1 sort, 2 exact re-scan
   uint32_t bs[kPer];
   uint32_t* s_bstart = s_bstart_all[wave];
   uint32_t last = 0;
   if (linear) {
     // histogram; the returned count is the key's slot inside its bucket. Every
-    // slot issues its atomic (invalid ones add 0 to this lane's dummy counter)
+    // slot issues its atomic (unkept ones add 0 to this lane's dummy counter)
     // so that the atomics go out back to back.
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const bool on = (vm >> q) & 1u;
-      const uint32_t b = on ? bucket_of(lk[q], vmax, scale) : (uint32_t)kBuckets + lane;
+      const uint32_t b = on ? bucket_of(yk[q], vmax, scale) : (uint32_t)kBuckets + lane;
       bs[q] = b | (atomicAdd(&s_bcount[b], on ? 1u : 0u) << 16);  // bucket | slot inside the bucket
     }
     __syncthreads();
@@ -1338,9 +1460,8 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     last = wave_reduce32(mine, MinOp{});  // the bucket of the meff-th key
     if (N < M && !all_kept) path = 2;
     else if (big > kBigBucket) path = 1;
+    else path = 0;
     wave_sync();
-  } else {
-    path = (theta_max == ~0ull || (!all_kept && kmax < theta_max)) ? 2 : 1;
   }
 
   if (path == 0) {
@@ -1354,7 +1475,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     for (int q = 0; q < kPer; ++q) start[q] = s_bstart[min(bs[q] & 0xffffu, (uint32_t)kBuckets - 1)];
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
-      if (((vm >> q) & 1u) && (bs[q] & 0xffffu) <= last) s_keys[start[q] + (bs[q] >> 16)] = lk[q];
+      if (((vm >> q) & 1u) && (bs[q] & 0xffffu) <= last) s_keys[start[q] + (bs[q] >> 16)] = yk[q];
     }
     __syncthreads();
     // rank inside the bucket; the softmax numerators (:286-290) in the same pass
@@ -1371,7 +1492,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     }
     __syncthreads();
   } else if (path == 1) {
-    const uint32_t N = sort_select(lk, vm, M, s_keys, s_top, ts);
+    const uint32_t N = sort_select(yk, vm, M, s_keys, s_top, ts);
     if (N < M && !all_kept) {
       path = 2;
     } else {
@@ -1393,7 +1514,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
   }
 
-  // 4. the chain after the top-M selection, in the first wavefront
+  // 5. the chain after the top-M selection, in the first wavefront
   if (wave != 0) return;
   uint32_t* scratch = (uint32_t*)s_keys;
   ChainBufs bf;
@@ -1445,7 +1566,7 @@ static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
   g->CH = best * tile;
   g->S = (V + g->CH - 1) / g->CH;
   const uint32_t W = g->S * kWavesPerBlock;
-  g->cap_w = floor_pow2(min(64u, (uint32_t)kUnionMax / W));
+  g->cap_w = floor_pow2(min(32u, (uint32_t)kUnionMax / W));
   const uint32_t cw = (3u * 256u + W - 1) / W + 6u;
   g->c_w = max(1u, min(g->cap_w / 2, cw));
   return true;
@@ -1493,6 +1614,7 @@ struct oxs_sampler {
   uint64_t* lists;
   uint64_t* wave_theta;
   uint32_t* wave_count;
+  uint64_t* libm;
   size_t bytes;
 };
 
@@ -1567,10 +1689,19 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
   const size_t b_lists = B * oxs::kUnionMax * sizeof(uint64_t);
   const size_t b_theta = B * W * sizeof(uint64_t);
   const size_t b_count = B * W * sizeof(uint32_t);
-  const bool ok = hipMalloc((void**)&s->lists, b_lists) == hipSuccess &&
+  bool ok = hipMalloc((void**)&s->lists, b_lists) == hipSuccess &&
                   hipMalloc((void**)&s->wave_theta, b_theta) == hipSuccess &&
-                  hipMalloc((void**)&s->wave_count, b_count) == hipSuccess;
-  s->bytes = b_lists + b_theta + b_count;
+                  hipMalloc((void**)&s->wave_count, b_count) == hipSuccess &&
+                  hipMalloc((void**)&s->libm, oxs::kLibmWords * sizeof(uint64_t)) == hipSuccess;
+  s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t);
+  if (ok) {  // the libm tables, as bit patterns, in the workspace
+    uint64_t host[oxs::kLibmWords];
+    ok = hipMemcpyFromSymbol(host, HIP_SYMBOL(oxs_libm::kExp2Tab), 32 * sizeof(uint64_t)) == hipSuccess &&
+         hipMemcpyFromSymbol(host + 32, HIP_SYMBOL(oxs_libm::kLogInvc), 16 * sizeof(double)) == hipSuccess &&
+         hipMemcpyFromSymbol(host + 48, HIP_SYMBOL(oxs_libm::kLnLogc), 16 * sizeof(double)) == hipSuccess &&
+         hipMemcpyFromSymbol(host + 64, HIP_SYMBOL(oxs_libm::kLog2Logc), 16 * sizeof(double)) == hipSuccess &&
+         hipMemcpy(s->libm, host, sizeof(host), hipMemcpyHostToDevice) == hipSuccess;
+  }
   if (!ok) {
     oxs_sampler_destroy(s);
     return OXS_ERR_HIP;
@@ -1584,6 +1715,7 @@ int oxs_sampler_destroy(oxs_sampler* s) {
   if (s->lists) (void)hipFree(s->lists);
   if (s->wave_theta) (void)hipFree(s->wave_theta);
   if (s->wave_count) (void)hipFree(s->wave_count);
+  if (s->libm) (void)hipFree(s->libm);
   free(s);
   return OXS_OK;
 }
@@ -1655,15 +1787,15 @@ int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
   p.lists = s->lists;
   p.wave_theta = s->wave_theta;
   p.wave_count = s->wave_count;
+  p.libm = s->libm;
   // Group rows by XCD when the batch divides evenly over the 8 XCDs.
   p.rpx = (b->batch % 8 == 0) ? b->batch / 8 : 0;
-  const uint32_t grid_a = b->batch * g.S;
-  const uint32_t grid_b = b->batch;
-
   const uint32_t epl = b->logits_dtype == OXS_DTYPE_F32 ? 4 : 8;
   const bool vec = ((uintptr_t)b->logits % 16 == 0) && ((size_t)b->logits_ld % epl == 0) &&
                    (b->vocab % epl == 0);
   const bool mask = b->allowed_mask != nullptr;
+  const uint32_t grid_a = b->batch * g.S;
+  const uint32_t grid_b = b->batch;
   hipStream_t st = (hipStream_t)stream;
   const hipError_t e = b->logits_dtype == OXS_DTYPE_F32
                            ? launch_all<OXS_DTYPE_F32>(g.slots, vec, mask, p, grid_a, grid_b, st)
