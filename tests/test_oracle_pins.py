@@ -167,6 +167,21 @@ def test_penalties_bias_ban_newline_temperature_brute_force(repeat_last_n):
     np.testing.assert_array_equal(r.logits_out[0].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("prefix", [[], [2], [2, 2, 1]])
+def test_dry_penalty_by_hand(prefix):
+    # sampler.rs:393-415 over the last dry_range = 6 ids [0, 1, 0, 1, 0, 1] (ids before them are
+    # out of range), multiplier 2, base 1.5, allowed length 2. Matches of the suffix and the id after them:
+    #   L=4: [0,1,0,1] at i=0 -> id 0, penalty 2 * 1.5^2 = 4.5
+    #   L=3: [1,0,1]   at i=1 -> id 0, penalty 3
+    #   L=2: [0,1]     at i=0 and i=2 -> id 0 twice, penalty 2 each
+    # so logit 0 goes 5 - 4.5 - 3 - 2 - 2 = -6.5 and ids 1, 2 keep 5.
+    history = prefix + [0, 1, 0, 1, 0, 1]
+    cfg = disabled_config(dry_multiplier=2.0, dry_base=1.5, dry_allowed_length=2, dry_range=6, temperature=0.0)
+    r = row([5.0, 5.0, 5.0], cfg, history, logits_out=True)
+    assert r.logits_out[0].tolist() == [-6.5, 5.0, 5.0]
+    assert int(r.tokens[0]) == 1  # greedy: ids 1 and 2 tie, the lower id wins
+
+
 def test_temperature_skipped_under_mirostat():
     # sampler.rs:249: no temperature scaling when Mirostat is on.
     lg = np.array([1.0, 2.5, -3.0, 0.25], np.float32)
