@@ -74,3 +74,59 @@ def test_config5_eight_steps(torch_gpu):
         g_hist, g_len, g_mu = g.history, g.history_len, g.mu
         r_hist, r_len, r_mu = r.history, r.history_len, r.mu
     assert int(r_len[0]) == 256 + 2 * w.steps  # two records per Mirostat step (sampler.rs:301, :307)
+
+
+def mixed_workload(B, V, seed):
+    """B rows cycling through every chain shape the config API offers, with ragged histories,
+    empty (all -inf) rows and a row whose history is already full."""
+    from oxide_sampler import SamplingConfig
+    rng = np.random.default_rng(seed)
+    logits = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+    spikes = rng.choice(V, min(V, 20), replace=False)
+    logits[:, spikes] += 6.0
+    if V > 64:
+        logits[:, 40:64] = np.float32(3.25)  # a run of equal logits: the lower id ranks first
+    base = [
+        wl.disabled_config(temperature=0.0),
+        wl.disabled_config(mirostat_mode=MirostatMode.V1, mirostat_tau=3.0, mirostat_eta=0.2, presence_penalty=0.3),
+        wl.disabled_config(mirostat_mode=MirostatMode.V2, repeat_penalty=1.2, repeat_last_n=32),
+        wl.disabled_config(min_p=0.02, xtc_threshold=0.05, xtc_probability=0.5, top_k=20),
+        wl.disabled_config(temperature=0.9, logit_biases={7 % V: 3.0, 11 % V: -2.0, V - 1: 5.0, V + 5: 1.0},
+                           banned_tokens={0, 3 % V, V + 2}, penalize_nl=True, newline_penalty=0.75),
+        wl.disabled_config(temperature=1.1, tfs_z=0.9, typical_p=0.8),
+        wl.disabled_config(temperature=0.8, top_k=300, top_p=0.97),
+        wl.disabled_config(temperature=1.5, top_k=1024),
+        SamplingConfig(),
+        wl.disabled_config(temperature=0.6, frequency_penalty=-0.5, presence_penalty=-0.2, repeat_penalty=0.8,
+                           repeat_last_n=0),
+    ]
+    configs = [base[i % len(base)] for i in range(B)]
+    cap = 300
+    history = rng.integers(0, V, size=(B, cap), dtype=np.uint32)
+    history[:, ::7] = np.uint32(min(10, V - 1))  # the newline id recurs
+    hlen = rng.integers(0, 200, size=B).astype(np.uint32)
+    hlen[min(5, B - 1)] = cap  # no room to record: OXS_ROW_HISTORY_FULL
+    if B > 13:
+        logits[13, :] = -np.inf  # OXS_ROW_EMPTY
+    mu = np.full(B, 10.0, np.float32)
+    return wl.Workload(name=f"mixed B={B} V={V}", logits=logits, dtype="f32", configs=configs, history=history,
+                       history_len=hlen, uniforms=wl.xorshift_uniforms(B, seed), mu=mu)
+
+
+@pytest.mark.parametrize("V", [1, 3, 257, 4097, 50001, 131072])
+def test_mixed_configs_ragged_vocab(torch_gpu, V):
+    B = 40 if V >= 4097 else 12
+    w = mixed_workload(B, V, seed=100 + V)
+    banner(f"mixed configs B={B} V={V}")
+    compare(run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=1024),
+            run_oracle(w, kept_ld=1024, logits_out=True), RTOL_F32, f"mixed V={V}")
+
+
+def test_mixed_configs_device_rng(torch_gpu):
+    # rng_state instead of uniforms: each drawing row advances its xorshift state by one step
+    w = mixed_workload(40, 32000, seed=7)
+    banner("mixed configs B=40 V=32000 device rng")
+    states = np.array([0x853C49E6748FEA9B ^ (i * 0x9E3779B97F4A7C15 & (2**64 - 1)) or 1 for i in range(40)],
+                      np.uint64)
+    compare(run_gpu(w, torch_gpu, kept_ld=1024, use_rng=True, rng_state=states, max_top_k=1024),
+            run_oracle(w, kept_ld=1024, use_rng=True, rng_state=states), RTOL_F32, "mixed rng")
