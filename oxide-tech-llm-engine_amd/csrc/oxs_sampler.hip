@@ -6,15 +6,15 @@
 //
 // stream_kernel (grid: rows x chunks). Each block streams CH logits of one row
 //   with coalesced 16-byte loads and keeps only a small candidate set per
-//   wavefront. Dense stages (mask, temperature) are applied in registers. The
+//   wavefront. The dense stage (grammar mask) is applied in registers. The
 //   sparse stages (bans, biases, newline, repetition/frequency/presence over
-//   the history window) touch few ids; the block marks those ids in an LDS
-//   bitmap, leaves them out of the stream, and computes their exact values in
-//   a short pass at the end. Each wavefront finds the c-th largest of its 64
-//   lane maxima (32 ballot steps) and writes every unmarked element at or above
-//   it, plus its share of the marked ones, as 64-bit keys
-//   (order-preserving value bits << 32 | ~token id): keys are unique and order
-//   candidates by value descending, then lower token id.
+//   the history window) touch few ids: while the second half of the chunk is
+//   still in flight, the block hashes those ids in LDS; once the values are
+//   staged in LDS, one thread per hash entry writes its id's exact value. Each
+//   wavefront finds a lower bound of the c-th largest of its 64 lane maxima
+//   (16 ballot steps) and writes every value at or above it as a 64-bit key
+//   (order-preserving bits of value * inv_temp << 32 | ~token id): keys are
+//   unique and order candidates by value descending, then lower token id.
 //
 // tail_kernel (one block per row). Reads the row's candidate keys and the
 //   wavefront thresholds into registers; if at least M = max(top_k, 256) keys
@@ -126,15 +126,6 @@ __device__ __forceinline__ uint32_t grouped_index(uint32_t block, uint32_t per_x
 
 // ---------------------------------------------------------------- row setup
 
-// p[i], or dflt when p is null, read without a branch (from an in-bounds dummy
-// address when p is null): loads inside branches make the compiler wait for
-// every outstanding load at the branch's end.
-template <typename T>
-__device__ __forceinline__ T load_or(const T* ptr, size_t i, T dflt, const void* dummy) {
-  const T v = ptr ? ptr[i] : *(const T*)dummy;
-  return ptr ? v : dflt;
-}
-
 // Per-row constants of the pre-softmax stages (sampler.rs:184-254).
 struct RowXf {
   bool pen_rep, pen_fp, use_hist, nl_active, any_special, do_temp, dry;
@@ -172,10 +163,6 @@ __device__ __forceinline__ RowXf make_row_xf_h(const Params& p, const oxs_sampli
   return r;
 }
 
-__device__ __forceinline__ RowXf make_row_xf(const Params& p, const oxs_sampling_config& c,
-                                             uint32_t row) {
-  return make_row_xf_h(p, c, load_or<uint32_t>(p.history_len, row, 0u, p.configs));
-}
 
 // The sparse pre-softmax stages for one marked logit, in reference order:
 // ban (:184-188), bias (:189-193), newline (:196-200), repetition (:217-229),
@@ -233,6 +220,73 @@ __device__ __forceinline__ float load_logit(const Params& p, uint32_t row, uint3
 __device__ __forceinline__ bool mask_allows(const Params& p, uint32_t row, uint32_t idx) {
   const uint32_t w = p.mask[(size_t)row * p.mask_ld + (idx >> 5)];
   return (w >> (idx & 31)) & 1u;
+}
+
+// ---------------------------------------------------------------- scalar-cache row reads
+
+// The per-row record every lane needs (config, history length, uniform,
+// Mirostat mu, xorshift state) is read with scalar loads. Scalar loads count
+// on lgkmcnt, so waiting for them never waits for vector loads issued
+// earlier, which count on vmcnt in issue order. Loads only: nothing is
+// written through the scalar cache.
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x8v __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x16v __attribute__((ext_vector_type(16)));
+static_assert(sizeof(oxs_sampling_config) == 26 * 4, "SamplingConfig is 26 dwords");
+
+__device__ __forceinline__ uint64_t uniform_addr(const void* ptr) {
+  const uint64_t ad = (uint64_t)ptr;
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(ad >> 32)) << 32) |
+         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ad);
+}
+
+struct RowIn {
+  oxs_sampling_config cfg;
+  uint32_t history_len;
+  float uniform;
+  float mu;
+  uint64_t rng;
+};
+
+// Absent optional inputs read a valid dummy address (the config array) and
+// get their defaults.
+__device__ __forceinline__ RowIn load_row_in(const Params& p, uint32_t row) {
+  const void* dummy = p.configs;
+  const uint64_t a_cfg = uniform_addr(p.configs + ((p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row));
+  const uint64_t a_hl = uniform_addr(p.history_len ? (const void*)(p.history_len + row) : dummy);
+  const uint64_t a_u = uniform_addr(p.uniforms ? (const void*)(p.uniforms + row) : dummy);
+  const uint64_t a_mu = uniform_addr(p.mu ? (const void*)(p.mu + row) : dummy);
+  const uint64_t a_rng = uniform_addr(p.rng_state ? (const void*)(p.rng_state + row) : dummy);
+  u32x16v a;
+  u32x8v b;
+  u32x2v c, rng;
+  uint32_t hl, u, mu;
+  asm volatile(
+      "s_load_dwordx16 %0, %7, 0x0\n\t"
+      "s_load_dwordx8 %1, %7, 0x40\n\t"
+      "s_load_dwordx2 %2, %7, 0x60\n\t"
+      "s_load_dword %3, %8, 0x0\n\t"
+      "s_load_dword %4, %9, 0x0\n\t"
+      "s_load_dword %5, %10, 0x0\n\t"
+      "s_load_dwordx2 %6, %11, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(a), "=&s"(b), "=&s"(c), "=&s"(hl), "=&s"(u), "=&s"(mu), "=&s"(rng)
+      : "s"(a_cfg), "s"(a_hl), "s"(a_u), "s"(a_mu), "s"(a_rng)
+      : "memory");
+  uint32_t w[26];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) w[i] = a[i];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[16 + i] = b[i];
+  w[24] = c[0];
+  w[25] = c[1];
+  RowIn in;
+  memcpy(&in.cfg, w, sizeof(in.cfg));
+  in.history_len = p.history_len ? hl : 0u;
+  in.uniform = p.uniforms ? __uint_as_float(u) : 0.0f;
+  in.mu = p.mu ? __uint_as_float(mu) : 0.0f;
+  in.rng = p.rng_state ? (((uint64_t)rng[1] << 32) | rng[0]) : 0ull;
+  return in;
 }
 
 // ---------------------------------------------------------------- wavefront and block helpers
@@ -333,8 +387,8 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scrat
 // ---------------------------------------------------------------- marked ids (stream LDS hash)
 
 // A stream block marks the sparse-stage ids of its chunk (history window
-// with counts, bans, biases, newline) in an LDS bitmap and an open-addressing
-// hash keyed by chunk offset.
+// with counts, bans, biases, newline) in an open-addressing LDS hash keyed by
+// chunk offset.
 constexpr int kHashSlots = 256;
 constexpr uint32_t kEmptySlot = 0xffffffffu;
 __device__ __forceinline__ uint32_t hash_slot(uint32_t key) { return (key * 0x9e3779b1u) >> 24; }
@@ -366,12 +420,6 @@ __device__ __forceinline__ uint32_t hash_lookup(const uint32_t* hkeys, const uin
   return 0u;
 }
 
-// Marks one chunk offset: bitmap bit, then the hash entry.
-__device__ __forceinline__ bool mark_off(uint32_t* bitmap, uint32_t* hkeys, uint32_t* hvals, uint32_t off,
-                                         uint32_t add, uint32_t orv) {
-  atomicOr(&bitmap[off >> 5], 1u << (off & 31));
-  return hash_insert_from(hkeys, hvals, off, add, orv);
-}
 
 // ---------------------------------------------------------------- stream kernel
 
@@ -388,24 +436,21 @@ __device__ __forceinline__ void unit_of(const Params& p, uint32_t* row, uint32_t
   *chunk = k - *row * p.S;
 }
 
-__device__ __forceinline__ const oxs_sampling_config& row_config(const Params& p, uint32_t row) {
-  return p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
-}
 
-// One unit after its logits arrived. Dense stages (grammar mask, end of
-// vocabulary) in registers; the masked raw logits are staged in each thread's
-// own LDS slots. The logits whose sparse stages apply (history window, bans,
-// biases, newline) are marked in the chunk's LDS bitmap and hash and get their
-// exact values from the thread that holds them. Each wavefront finds a lower
-// bound of the c_w-th largest of its 64 lane maxima over the masked raw logits
-// and emits every logit at or above it as
-// (order key of x / temperature << 32 | ~token id); the threshold it reports
-// is in the same scaled values.
+// One unit after its logits arrived. The dense stages (grammar mask, end of
+// vocabulary) are applied in registers and the values are staged in LDS,
+// indexed by chunk offset. When the row has sparse-stage ids (history window,
+// bans, biases, newline), one thread per hash slot replaces its id's staged
+// value with the exact penalised one and every thread re-reads its values.
+// Each wavefront then finds a lower bound of the c_w-th largest of its 64 lane
+// maxima and emits every value at or above it as
+// (order key of x * inv_temp << 32 | ~token id). Thresholds and comparisons
+// use the unscaled values: x -> x * inv_temp is monotone for a finite positive
+// scale, and a row with any other scale is sent to the tail's exact path.
 template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
 __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint32_t chunk, const RowXf& r,
                                              const uint32_t (&raw)[SLOTS][(DT == OXS_DTYPE_F32) ? 4 : 8],
-                                             const uint32_t (&mw)[SLOTS], const uint32_t (&hv)[kHistUnroll],
-                                             float* s_x, uint32_t* s_bitmap, uint32_t* s_hkeys,
+                                             const uint32_t (&mw)[SLOTS], float* s_x, uint32_t* s_hkeys,
                                              uint32_t* s_hvals, uint32_t* s_full) {
   constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;
   constexpr int TILE = kThreads * EPL;
@@ -415,15 +460,10 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
   const uint32_t c0 = chunk * CH;
   const uint32_t c1 = min(c0 + CH, p.V);
   const float inv_t = r.do_temp ? r.inv_temp : 1.0f;
-  // Survivors are found on the masked raw logits when the temperature scale
-  // is a finite positive number (x -> x * inv_t is then monotone); only
-  // survivors are scaled. Otherwise they are found on the scaled values.
-  const bool wy = WB || inv_t == 1.0f || !(inv_t > 0.0f && inv_t <= __FLT_MAX__);
-  auto wval = [=](float x) { return wy ? x * inv_t : x; };
+  const bool scale_ok = inv_t > 0.0f && inv_t <= __FLT_MAX__;
 
-  // ---- masked raw logits, staged in this thread's LDS slots; lane maximum
+  // ---- masked raw logits, staged in LDS at their chunk offsets
   float v[NE];
-  float lmax = neg_inf();
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s) {
     const uint32_t off = s * TILE + tid * EPL;  // chunk-local
@@ -432,66 +472,58 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
       float x = __uint_as_float(raw[s][e]);
       if (MASK && !((mw[s] >> ((c0 + off + e) & 31)) & 1u)) x = neg_inf();
       if (!VEC && c0 + off + e >= c1) x = neg_inf();
-      if (VEC && c0 + off >= c1) x = neg_inf();  // past the end of a short last chunk
       v[s * EPL + e] = x;
-      lmax = fmaxf(lmax, wval(x));  // a NaN here only lowers the pruning, never correctness
-      if (WB && c0 + off + e < c1) p.logits_out[(size_t)row * p.logits_out_ld + c0 + off + e] = x * inv_t;
     }
+  }
+  if (VEC && c1 - c0 < CH) {  // a short last chunk: groups past the end are dropped
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s)
+      if (c0 + s * TILE + tid * EPL >= c1) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[s * EPL + e] = neg_inf();
+      }
+  }
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s)
 #pragma unroll
     for (int e = 0; e < EPL; e += 4)
-      *(float4*)&s_x[(s * kThreads + tid) * EPL + e] =
+      *(float4*)&s_x[s * TILE + tid * EPL + e] =
           make_float4(v[s * EPL + e], v[s * EPL + e + 1], v[s * EPL + e + 2], v[s * EPL + e + 3]);
-  }
 
-  // ---- sparse-stage ids of this chunk: bitmap and hash (a count per history
-  // window occurrence, a flag per ban, bias, newline); the first claim of
-  // every window id's home slot goes out at once, collisions after
-  uint32_t umask = 0;
+  // ---- sparse-stage ids at their exact values (sampler.rs:184-245)
   if (r.any_special) {
-    bool ok = true;
-    uint32_t prev[kHistUnroll];
-#pragma unroll
-    for (int q = 0; q < kHistUnroll; ++q) {
-      const uint32_t t = r.use_hist && tid + q * kThreads < r.wn ? hv[q] : 0xffffffffu;
-      const bool in = t >= c0 && t < c1;
-      prev[q] = in ? atomicCAS(&s_hkeys[hash_slot(t - c0)], kEmptySlot, t - c0) : 0u;
-      if (in) atomicOr(&s_bitmap[(t - c0) >> 5], 1u << ((t - c0) & 31));
+    __syncthreads();  // values staged, marks complete
+    for (uint32_t h = tid; h < (uint32_t)kHashSlots; h += kThreads) {
+      const uint32_t off = s_hkeys[h];
+      if (off != kEmptySlot) s_x[off] = apply_special(p.bias_ids, p.bias_values, r, s_x[off], s_hvals[h], c0 + off);
     }
+    __syncthreads();
 #pragma unroll
-    for (int q = 0; q < kHistUnroll; ++q) {
-      const uint32_t t = r.use_hist && tid + q * kThreads < r.wn ? hv[q] : 0xffffffffu;
-      if (!(t >= c0 && t < c1)) continue;
-      if (prev[q] == kEmptySlot || prev[q] == t - c0) atomicAdd(&s_hvals[hash_slot(t - c0)], 1u);
-      else ok &= hash_insert_from(s_hkeys, s_hvals, t - c0, 1u, 0u);
-    }
-    if (r.use_hist) {
-      const uint32_t* hrow = p.history + (size_t)row * p.history_ld + r.wstart;
-      for (uint32_t j = tid + kHistUnroll * kThreads; j < r.wn; j += kThreads) {  // long windows
-        const uint32_t t = hrow[j];
-        if (t >= c0 && t < c1) ok &= mark_off(s_bitmap, s_hkeys, s_hvals, t - c0, 1u, 0u);
+    for (int s = 0; s < SLOTS; ++s)
+#pragma unroll
+      for (int e = 0; e < EPL; e += 4) {
+        const float4 q = *(const float4*)&s_x[s * TILE + tid * EPL + e];
+        v[s * EPL + e] = q.x;
+        v[s * EPL + e + 1] = q.y;
+        v[s * EPL + e + 2] = q.z;
+        v[s * EPL + e + 3] = q.w;
       }
-    }
-    for (uint32_t k = tid; k < r.ban_cnt; k += kThreads) {
-      const uint32_t id = p.ban_ids[r.ban_off + k];
-      if (id >= c0 && id < c1) ok &= mark_off(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBanFlag);
-    }
-    for (uint32_t k = tid; k < r.bias_cnt; k += kThreads) {
-      const uint32_t id = p.bias_ids[r.bias_off + k];
-      if (id >= c0 && id < c1) ok &= mark_off(s_bitmap, s_hkeys, s_hvals, id - c0, 0u, kBiasFlag);
-    }
-    if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1)
-      ok &= mark_off(s_bitmap, s_hkeys, s_hvals, r.nl_id - c0, 0u, kNlFlag);
-    if (!ok) *s_full = 1;
-    __syncthreads();  // marks complete
+  }
+  if (WB) {  // what the reference leaves in its logits argument (temperature included)
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const uint32_t off = s * TILE + tid * EPL;
-      umask |= ((s_bitmap[off >> 5] >> (off & 31)) & ((1u << EPL) - 1u)) << (s * EPL);
-    }
+    for (int s = 0; s < SLOTS; ++s)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const uint32_t idx = c0 + s * TILE + tid * EPL + e;
+        if (idx < c1) p.logits_out[(size_t)row * p.logits_out_ld + idx] = v[s * EPL + e] * inv_t;
+      }
   }
 
   // ---- wavefront threshold: a lower bound of the c_w-th largest lane
   // maximum, from the top 16 bits of the order keys
+  float lmax = v[0];
+#pragma unroll
+  for (int i = 1; i < NE; ++i) lmax = fmaxf(lmax, v[i]);  // a NaN only lowers the pruning
   const uint32_t lm = f2ord(lmax);
   uint32_t theta = 0;
 #pragma unroll
@@ -507,13 +539,12 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
     th_ord = kMinValidOrd;
   } else {
     theta_f = ord2f(theta);
-    // unemitted logits are < theta_f, so their scaled values are <= theta_f * inv_t
-    th_ord = wy ? theta : f2ord(theta_f * inv_t) + 1u;
+    // unemitted values are < theta_f, so their scaled values are <= theta_f * inv_t
+    th_ord = inv_t == 1.0f ? theta : f2ord(theta_f * inv_t) + 1u;
   }
-  uint32_t smask = 0;  // bit i: wval(x_i) >= theta_f (false for -inf and NaN), unmarked
+  uint32_t smask = 0;  // bit i: v[i] >= theta_f (false for -inf and NaN)
 #pragma unroll
-  for (int i = 0; i < NE; ++i) smask |= (wval(v[i]) >= theta_f ? 1u : 0u) << i;
-  smask &= ~umask;
+  for (int i = 0; i < NE; ++i) smask |= (v[i] >= theta_f ? 1u : 0u) << i;
 
   // ---- survivors into this wavefront's list; slots from the wavefront's
   // ballot of the lanes that emit, in lane order
@@ -528,10 +559,10 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
       const uint32_t b = __builtin_ctz(smask);
       smask &= smask - 1u;
       const uint32_t sl = b / EPL, e = b % EPL;
-      const float y = s_x[(sl * kThreads + tid) * EPL + e] * inv_t;
-      const uint32_t k = cand_key(y);
+      const uint32_t off = sl * TILE + tid * EPL + e;
+      const uint32_t k = cand_key(s_x[off] * inv_t);
       want = k != 0u;
-      key = comp_key(k, c0 + sl * TILE + tid * EPL + e);
+      key = comp_key(k, c0 + off);
     }
     const uint64_t m = __ballot(want);
     if (want) {
@@ -540,56 +571,74 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
     }
     base += (uint32_t)__popcll(m);
   }
-
-  // ---- this thread's marked logits at their exact values (sampler.rs:184-254)
-  if (r.any_special) {
-    while (true) {
-      if (__ballot(umask != 0u) == 0) break;
-      bool want = false;
-      uint64_t key = 0;
-      if (umask) {
-        const uint32_t b = __builtin_ctz(umask);
-        umask &= umask - 1u;
-        const uint32_t sl = b / EPL, e = b % EPL;
-        const uint32_t off = sl * TILE + tid * EPL + e;
-        float y = apply_special(p.bias_ids, p.bias_values, r, s_x[(sl * kThreads + tid) * EPL + e],
-                                hash_lookup(s_hkeys, s_hvals, off), c0 + off);
-        y *= inv_t;
-        if (WB && c0 + off < c1) p.logits_out[(size_t)row * p.logits_out_ld + c0 + off] = y;
-        const uint32_t k = cand_key(y);
-        want = k != 0u && k >= th_ord;
-        key = comp_key(k, c0 + off);
-      }
-      const uint64_t m = __ballot(want);
-      if (want) {
-        const uint32_t q = base + lanes_below(m);
-        if (q < p.cap_w) out[q] = key;
-      }
-      base += (uint32_t)__popcll(m);
-    }
-  }
   if (lane == 0) {
-    const bool bad = base > p.cap_w || (r.any_special && *s_full != 0u);
+    const bool bad = base > p.cap_w || (r.any_special && *s_full != 0u) || !scale_ok;
     p.wave_theta[wslot] = bad ? ~0ull : ((uint64_t)th_ord << 32);
     p.wave_count[wslot] = bad ? 0u : base;
   }
 }
 
-// One (row, chunk) per block: the row's history length and config first,
-// the chunk's logits and mask words, then the history window ids (the
-// sparse-stage marks need them only after the logits are in).
+// The chunk's sparse-stage ids into the LDS hash: a count per
+// history window occurrence, a flag per ban, bias and newline. The first claim
+// of every window id's home slot goes out at once, collisions after. Ends
+// with no barrier: the next block barrier completes the marks.
+__device__ __forceinline__ void build_marks(const Params& p, const RowXf& r, uint32_t row, uint32_t c0,
+                                            uint32_t c1, const uint32_t (&hv)[kHistUnroll],
+                                            uint32_t* s_hkeys, uint32_t* s_hvals, uint32_t* s_full) {
+  const uint32_t tid = threadIdx.x;
+  bool ok = true;
+  uint32_t prev[kHistUnroll];
+#pragma unroll
+  for (int q = 0; q < kHistUnroll; ++q) {
+    const uint32_t t = r.use_hist && tid + q * kThreads < r.wn ? hv[q] : 0xffffffffu;
+    const bool in = t >= c0 && t < c1;
+    prev[q] = in ? atomicCAS(&s_hkeys[hash_slot(t - c0)], kEmptySlot, t - c0) : 0u;
+  }
+#pragma unroll
+  for (int q = 0; q < kHistUnroll; ++q) {
+    const uint32_t t = r.use_hist && tid + q * kThreads < r.wn ? hv[q] : 0xffffffffu;
+    if (!(t >= c0 && t < c1)) continue;
+    if (prev[q] == kEmptySlot || prev[q] == t - c0) atomicAdd(&s_hvals[hash_slot(t - c0)], 1u);
+    else ok &= hash_insert_from(s_hkeys, s_hvals, t - c0, 1u, 0u);
+  }
+  if (r.use_hist) {
+    const uint32_t* hrow = p.history + (size_t)row * p.history_ld + r.wstart;
+    for (uint32_t j = tid + kHistUnroll * kThreads; j < r.wn; j += kThreads) {  // long windows
+      const uint32_t t = hrow[j];
+      if (t >= c0 && t < c1) ok &= hash_insert_from(s_hkeys, s_hvals, t - c0, 1u, 0u);
+    }
+  }
+  for (uint32_t k = tid; k < r.ban_cnt; k += kThreads) {
+    const uint32_t id = p.ban_ids[r.ban_off + k];
+    if (id >= c0 && id < c1) ok &= hash_insert_from(s_hkeys, s_hvals, id - c0, 0u, kBanFlag);
+  }
+  for (uint32_t k = tid; k < r.bias_cnt; k += kThreads) {
+    const uint32_t id = p.bias_ids[r.bias_off + k];
+    if (id >= c0 && id < c1) ok &= hash_insert_from(s_hkeys, s_hvals, id - c0, 0u, kBiasFlag);
+  }
+  if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1)
+    ok &= hash_insert_from(s_hkeys, s_hvals, r.nl_id - c0, 0u, kNlFlag);
+  if (!ok) *s_full = 1;
+}
+
+// One (row, chunk) per block. The first half of the chunk's logits is issued
+// at once (its addresses need nothing from memory); the row's record comes
+// through the scalar cache meanwhile; then the history window ids and the
+// second half. The marks are built when the window ids arrive, which waits
+// for the first half only (vector loads complete in issue order), while the
+// second half is still in flight.
 template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
 __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
   constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;  // logits per 16-byte load
   constexpr int TILE = kThreads * EPL;
   constexpr int CH = SLOTS * TILE;
   constexpr int NE = SLOTS * EPL;  // logits per lane
+  constexpr int H1 = (SLOTS + 1) / 2;  // loads issued before the row's record is read
   constexpr size_t ESZ = (DT == OXS_DTYPE_F32) ? 4 : 2;
   static_assert(CH <= kMaxChunk, "chunk too large");
   static_assert(NE <= 32, "one survivor bit per logit of a lane");
 
   __shared__ __align__(16) float s_x[NE * kThreads];  // each thread's masked raw logits (private slots)
-  __shared__ uint32_t s_bitmap[CH / 32];              // marked (sparse-stage) ids of the chunk
   __shared__ uint32_t s_hkeys[kHashSlots];
   __shared__ uint32_t s_hvals[kHashSlots];
   __shared__ uint32_t s_full;
@@ -600,13 +649,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
   if (row >= p.B) return;
   const uint32_t c0 = chunk * CH;
   const uint32_t c1 = min(c0 + (uint32_t)CH, p.V);
-  const RowXf r = make_row_xf(p, row_config(p, row), row);
-  __builtin_amdgcn_sched_barrier(0);
 
   uint32_t raw[SLOTS][EPL];
   const char* rowp = (const char*)p.logits + (size_t)row * (size_t)p.ld * ESZ;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
+  auto load_slot = [&](int s) {
     const uint32_t base = c0 + s * TILE + tid * EPL;
     if constexpr (VEC) {
       // V is a multiple of EPL here: past-the-end groups re-read the row's
@@ -628,8 +674,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
         raw[s][e] = __float_as_uint(load_logit<DT>(p, row, idx < c1 ? idx : p.V - 1));
       }
     }
-  }
+  };
   uint32_t mw[SLOTS];
+#pragma unroll
+  for (int s = 0; s < H1; ++s) load_slot(s);
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s) {
     mw[s] = 0xffffffffu;
@@ -638,9 +686,16 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
       mw[s] = p.mask[(size_t)row * p.mask_ld + ((b2 < c1 ? b2 : p.V - 1) >> 5)];
     }
   }
+  for (uint32_t i = tid; i < (uint32_t)kHashSlots; i += kThreads) {
+    s_hkeys[i] = kEmptySlot;
+    s_hvals[i] = 0;
+  }
+  if (tid == 0) s_full = 0;
+  __builtin_amdgcn_sched_barrier(0);
+  const RowIn rin = load_row_in(p, row);
+  const RowXf r = make_row_xf_h(p, rin.cfg, rin.history_len);
   // history window ids, read without a branch (an in-bounds dummy address
-  // where the row has none): unconditional reads keep the waits on the
-  // logits exact
+  // where the row has none)
   uint32_t hv[kHistUnroll];
   const uint32_t* hsrc = r.use_hist ? p.history + (size_t)row * p.history_ld + r.wstart : (const uint32_t*)p.configs;
   const uint32_t hn = r.use_hist ? r.wn : 0u;
@@ -649,18 +704,15 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
     const uint32_t j = tid + q * kThreads;
     hv[q] = hsrc[j < hn ? j : 0u];
   }
-  if (r.any_special) {  // tables cleared while the reads are in flight
-    for (uint32_t i = tid; i < (uint32_t)CH / 32; i += kThreads) s_bitmap[i] = 0;
-    for (uint32_t i = tid; i < (uint32_t)kHashSlots; i += kThreads) {
-      s_hkeys[i] = kEmptySlot;
-      s_hvals[i] = 0;
-    }
-    if (tid == 0) s_full = 0;
-    __syncthreads();
-  }
+#pragma unroll
+  for (int s = H1; s < SLOTS; ++s) load_slot(s);
   __builtin_amdgcn_sched_barrier(0);
+  if (r.any_special) {
+    __syncthreads();  // tables cleared
+    build_marks(p, r, row, c0, c1, hv, s_hkeys, s_hvals, &s_full);
+  }
 
-  process_unit<DT, SLOTS, VEC, MASK, WB>(p, row, chunk, r, raw, mw, hv, s_x, s_bitmap, s_hkeys, s_hvals, &s_full);
+  process_unit<DT, SLOTS, VEC, MASK, WB>(p, row, chunk, r, raw, mw, s_x, s_hkeys, s_hvals, &s_full);
 }
 
 // ---------------------------------------------------------------- tail helpers
@@ -1328,16 +1380,12 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   const uint32_t row = p.rpx ? grouped_index(blockIdx.x, p.rpx) : blockIdx.x;
   if (row >= p.B) return;
 
-  // 1. every global read of the row, issued before anything waits: the
-  // config, the wavefront thresholds, the candidate slots (two per 16-byte
-  // load) with the count of the wavefront that wrote them, the history
-  // window, the chain's per-row state and the libm tables (into LDS)
-  // (reads whose values are needed first are issued first: a wait covers
-  // every read issued before the one it waits for)
-  const oxs_sampling_config c = p.configs[(p.flags & OXS_FLAG_SHARED_CONFIG) ? 0 : row];
-  const uint32_t hlen0 = load_or<uint32_t>(p.history_len, row, 0u, p.configs);
-  const LibmEntries tabv = fetch_libm_tables(p.libm);
-  const RowXf r = make_row_xf_h(p, c, hlen0);
+  // 1. the row's reads, issued before anything waits: the wavefront
+  // thresholds, the candidate slots (two per 16-byte load) with the count of
+  // the wavefront that wrote them and the libm tables (vector loads whose
+  // addresses need nothing from memory), then the row's record (config,
+  // history length, uniform, mu, rng) through the scalar cache, whose wait
+  // does not cover the vector loads
   const uint32_t W = p.S * kWavesPerBlock;
   const uint32_t span = W * p.cap_w;  // even: cap_w >= 8
   const uint64_t wt0 = p.wave_theta[(size_t)row * W + (tid < W ? tid : 0u)];
@@ -1354,13 +1402,17 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     lk[2 * q + 1] = k2.y;
     lc[q] = wcrow[(2u * at) >> p.cap_shift];
   }
+  const LibmEntries tabv = fetch_libm_tables(p.libm);
+  __builtin_amdgcn_sched_barrier(0);  // every vector read above is issued before anything waits
+  const RowIn rin = load_row_in(p, row);
+  const oxs_sampling_config c = rin.cfg;
+  const RowXf r = make_row_xf_h(p, c, rin.history_len);
   RowState rs;
-  rs.uniform = load_or<float>(p.uniforms, row, 0.0f, p.configs);
-  rs.mu = load_or<float>(p.mu, row, 0.0f, p.configs);
-  rs.rng = load_or<uint64_t>(p.rng_state, row, 0ull, p.configs);
-  rs.history_len = hlen0;
+  rs.uniform = rin.uniform;
+  rs.mu = rin.mu;
+  rs.rng = rin.rng;
+  rs.history_len = rin.history_len;
   const uint64_t wt = tid < W ? wt0 : 0ull;
-  __builtin_amdgcn_sched_barrier(0);  // every read above is issued before anything waits
   store_libm_tables(tabv, s_tab);
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
 
