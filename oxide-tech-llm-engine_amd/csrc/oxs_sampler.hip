@@ -771,7 +771,7 @@ __device__ void find_digit(const uint32_t* hist, TailShared& ts, uint32_t kk) {
 
 // Dense penalty table of logits [c0, c1) for the exact path: window counts in
 // the low bits, ban/bias/newline flags in the high bits. Ends with a barrier.
-__device__ void build_table(const Params& p, const RowXf& r, uint32_t row, uint32_t c0,
+__device__ __forceinline__ void build_table(const Params& p, const RowXf& r, uint32_t row, uint32_t c0,
                             uint32_t c1, uint32_t* table) {
   const uint32_t tid = threadIdx.x;
   for (uint32_t i = tid; i < c1 - c0; i += kThreads) table[i] = 0;
@@ -814,7 +814,7 @@ __device__ __forceinline__ float transformed_logit(const Params& p, const RowXf&
 // keys cannot be proven to hold the row's top M. Writes the top min(M, pool)
 // keys to out (unordered); returns that count.
 template <int DT>
-__device__ uint32_t exact_select_row(const Params& p, const RowXf& r, uint32_t row, uint32_t M,
+__device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowXf& r, uint32_t row, uint32_t M,
                                      uint32_t* table, uint32_t* hist, uint64_t* out,
                                      TailShared& ts) {
   const uint32_t tid = threadIdx.x;
@@ -931,14 +931,19 @@ struct Scaled {
   float k;
   __device__ float operator()(float v) const { return v * k; }
 };
+// (v * k1) * k2 with both products rounded, as two successive scalings.
+struct Scaled2 {
+  float k1, k2;
+  __device__ float operator()(float v) const { return (v * k1) * k2; }
+};
+
+__device__ __forceinline__ float4 ld4(const float* a) { return *(const float4*)a; }
 
 struct Chain {
   uint32_t stop;  // index + 1 of the element that reached the stop value, else n
   float sum;      // running sum there, else the total
   bool hit;
 };
-
-__device__ __forceinline__ float4 ld4(const float* a) { return *(const float4*)a; }
 
 // 16 ordered adds of one group; t[j] is the running sum after element j.
 template <typename F>
@@ -1045,7 +1050,7 @@ __device__ __forceinline__ Chain seq_chain(const float* a, uint32_t n, float ini
   return Chain{n, s, false};
 }
 
-__device__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status) {
+__device__ __forceinline__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status) {
   if (threadIdx.x == 0) {
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
@@ -1114,7 +1119,7 @@ __device__ __forceinline__ uint32_t wave_compact(uint32_t* ids, float* pr, uint3
 // block barriers: parallel stages split the candidates over the lanes; the
 // reference's ordered sums run in every lane at once (seq_chain), so each lane
 // holds each result.
-__device__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32_t row, uint32_t n,
+__device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32_t row, uint32_t n,
                            ChainBufs bf, const RowState& rs, const LibmTables& tab) {
   const uint32_t l = threadIdx.x;
   uint32_t* ids = bf.ids;
@@ -1128,9 +1133,29 @@ __device__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32
   uint32_t len = n, n_record = 1, token;
   float inv_total = 1.0f;
   const bool mirostat = c.mirostat_mode == OXS_MIROSTAT_V1 || c.mirostat_mode == OXS_MIROSTAT_V2;
-  // Min-p (:315-319): keep p >= p_max * min_p, in order; the pass also turns
-  // the exps into probabilities.
-  if (!mirostat && c.min_p > 0.0f && len > 0) {
+  // While every stage keeps a prefix of the sorted list (min-p, top-k, top-p)
+  // the probabilities p_i = exp_i * inv_sum stay implicit: each reader scales
+  // by k_in. p is non-increasing, so min-p's retain (:315-319) keeps a prefix,
+  // found by counting. XTC, tail-free, typical and Mirostat get the
+  // probabilities written out first (k_in = 1, and v * 1 is v).
+  const bool lazy = !mirostat && !(c.xtc_probability > 0.0f) && !(c.tfs_z < 1.0f) && !(c.typical_p < 1.0f) &&
+                    sum_exp > 0.0f && sum_exp <= __FLT_MAX__;
+  const float k_in = lazy ? inv_sum : 1.0f;
+  if (lazy) {
+    if (c.min_p > 0.0f && len > 0) {
+      const float threshold = to_prob(pr[0]) * c.min_p;
+      uint32_t cnt = 0;
+      for (uint32_t r0 = 0; r0 < n; r0 += 64) {
+        const uint32_t i = r0 + l;
+        const uint64_t m = __ballot(i < n && to_prob(pr[i < n ? i : 0u]) >= threshold);
+        cnt += (uint32_t)__popcll(m);
+        if (m != ~0ull) break;  // the prefix ended
+      }
+      len = cnt;
+    }
+  } else if (!mirostat && c.min_p > 0.0f && len > 0) {
+    // Min-p (:315-319): keep p >= p_max * min_p, in order; the pass also turns
+    // the exps into probabilities.
     const float threshold = to_prob(pr[0]) * c.min_p;
     len = wave_compact(ids, pr, len, to_prob, [=](float v) { return v >= threshold; });
   } else {
@@ -1271,8 +1296,8 @@ __device__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32
     // Top-p (:346-357) cuts at the first running sum >= top_p; the
     // renormalisation total (:360-368) is the running sum at that cut.
     {
-      const Chain ch = c.top_p < 1.0f ? seq_chain<true>(pr, len, 0.0f, c.top_p, Ident{}, bf.hit)
-                                      : seq_chain<false>(pr, len, 0.0f, 0.0f, Ident{}, bf.hit);
+      const Chain ch = c.top_p < 1.0f ? seq_chain<true>(pr, len, 0.0f, c.top_p, Scaled{k_in}, bf.hit)
+                                      : seq_chain<false>(pr, len, 0.0f, 0.0f, Scaled{k_in}, bf.hit);
       len = ch.stop;
       inv_total = ch.sum > 0.0f ? 1.0f / ch.sum : 1.0f;
     }
@@ -1289,7 +1314,7 @@ __device__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32
         rnd = next_f32(&st);
         if (l == 0) p.rng_state[row] = st;
       }
-      const Chain ch = seq_chain<true>(pr, len, 0.0f, rnd, Scaled{inv_total}, bf.hit);
+      const Chain ch = seq_chain<true>(pr, len, 0.0f, rnd, Scaled2{k_in, inv_total}, bf.hit);
       token = ch.hit ? ids[ch.stop - 1] : (len ? ids[0] : 0u);
     }
   }
@@ -1315,7 +1340,7 @@ __device__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32
   const uint32_t nk = (uint32_t)min((int64_t)len, p.kept_ld);
   for (uint32_t i = l; i < nk; i += 64) {
     if (p.out_kept_ids) p.out_kept_ids[(size_t)row * p.kept_ld + i] = ids[i];
-    if (p.out_kept_probs) p.out_kept_probs[(size_t)row * p.kept_ld + i] = pr[i] * inv_total;
+    if (p.out_kept_probs) p.out_kept_probs[(size_t)row * p.kept_ld + i] = (pr[i] * k_in) * inv_total;
   }
 }
 
