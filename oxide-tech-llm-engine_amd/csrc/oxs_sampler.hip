@@ -47,6 +47,7 @@ constexpr int kMaxM = 1024;       // largest max(top_k, 256) run on the device
 constexpr int kMaxChunk = 8192;   // logits per stream block
 constexpr int kMaxChunks = 64;    // chunks per row
 constexpr int kBuckets = 256;     // tail counting-sort buckets
+constexpr int kRecPer = kMaxChunks * kWavesPerBlock / 64;  // wavefront records per lane a tail wavefront reads
 constexpr int kHistUnroll = 4;    // history-window ids per stream thread read with the logits
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -90,7 +91,7 @@ struct Params {
   uint32_t rpx;    // rows per XCD when rows are grouped by XCD, else 0
   // workspace
   uint64_t* lists;       // [B][S*4][cap_w]
-  uint64_t* wave_theta;  // [B][S*4]
+  uint64_t* wave_theta;  // [B][S*4] wavefront records: threshold << 32 | largest key
   uint32_t* wave_count;  // [B][S*4]
   const uint64_t* libm;  // [kLibmWords]: the libm tables (exp2, 1/c, ln c, log2 c) as bit patterns
 };
@@ -424,7 +425,6 @@ __device__ __forceinline__ uint32_t hash_lookup(const uint32_t* hkeys, const uin
 // ---------------------------------------------------------------- stream kernel
 
 constexpr uint32_t kMinValidOrd = 0x00800000u;  // f2ord(-FLT_MAX): every candidate key is >= this
-constexpr uint64_t kAllValid = (uint64_t)kMinValidOrd << 32;  // threshold of a wavefront that kept all
 
 // The (row, chunk) of a stream block. With rpx > 0 the hardware's round-robin
 // placement of blocks on the 8 XCDs (block i on XCD i % 8) gives XCD x the
@@ -571,9 +571,10 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
     }
     base += (uint32_t)__popcll(m);
   }
+  const uint32_t kmax32 = cand_key(ord2f(wave_max_u32(lm)) * inv_t);  // the wavefront's largest key
   if (lane == 0) {
     const bool bad = base > p.cap_w || (r.any_special && *s_full != 0u) || !scale_ok;
-    p.wave_theta[wslot] = bad ? ~0ull : ((uint64_t)th_ord << 32);
+    p.wave_theta[wslot] = bad ? ~0ull : (((uint64_t)th_ord << 32) | kmax32);
     p.wave_count[wslot] = bad ? 0u : base;
   }
 }
@@ -718,9 +719,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
 // ---------------------------------------------------------------- tail helpers
 
 struct TailShared {
-  uint64_t a_theta[kWavesPerBlock];  // per-wavefront partials of the first reduction
-  uint64_t a_kmax[kWavesPerBlock];
-  uint64_t a_kmin[kWavesPerBlock];
+  uint64_t a_kmin[kWavesPerBlock];  // per-wavefront smallest valid keys
   uint32_t scan_scratch[8];
   uint32_t sel_digit, sel_above, sel_count, counter;
 };
@@ -1413,7 +1412,12 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   // does not cover the vector loads
   const uint32_t W = p.S * kWavesPerBlock;
   const uint32_t span = W * p.cap_w;  // even: cap_w >= 8
-  const uint64_t wt0 = p.wave_theta[(size_t)row * W + (tid < W ? tid : 0u)];
+  uint64_t wr[kRecPer];  // every wavefront reads all W records (lane + 64 q; clamped repeats change no maximum)
+#pragma unroll
+  for (int q = 0; q < kRecPer; ++q) {
+    const uint32_t w = lane + 64u * q;
+    wr[q] = p.wave_theta[(size_t)row * W + (w < W ? w : W - 1u)];
+  }
   uint64_t lk[kPer];
   uint32_t lc[kPer / 2];
   const ulonglong2* lrow = (const ulonglong2*)(p.lists + (size_t)row * span);
@@ -1437,7 +1441,6 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   rs.mu = rin.mu;
   rs.rng = rin.rng;
   rs.history_len = rin.history_len;
-  const uint64_t wt = tid < W ? wt0 : 0ull;
   store_libm_tables(tabv, s_tab);
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
 
@@ -1452,39 +1455,44 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     return;
   }
 
-  // 2. the largest wavefront threshold, and the largest and smallest valid key
-  uint64_t kmx = 0, kmn = ~0ull;
+  // 2. the largest wavefront threshold and the largest key, from the
+  // wavefront records, reduced by every wavefront on its own (a record of all
+  // ones marks a wavefront whose candidates are incomplete: the exact path);
+  // the smallest valid key is needed only when every wavefront kept all of
+  // its candidates
   uint32_t valid = 0;
+  uint64_t kmn = ~0ull;
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const uint32_t slot = 2u * (tid + (q / 2) * kThreads) + (q & 1);
     const uint64_t k = lk[q];
     if (slot < span && (slot & (p.cap_w - 1u)) < lc[q / 2] && k != 0ull) {
       valid |= 1u << q;
-      kmx = k > kmx ? k : kmx;
       kmn = k < kmn ? k : kmn;
     }
   }
-  {
-    const uint64_t a = wave_max_u64(wt), b = wave_max_u64(kmx), d = wave_min_u64(kmn);
-    if (lane == 0) {
-      ts.a_theta[wave] = a;
-      ts.a_kmax[wave] = b;
-      ts.a_kmin[wave] = d;
-    }
-  }
-  __syncthreads();
-  uint64_t theta_max = ts.a_theta[0], kmax = ts.a_kmax[0], kmin = ts.a_kmin[0];
+  uint32_t th_l = 0, km_l = 0;
 #pragma unroll
-  for (int w = 1; w < kWavesPerBlock; ++w) {
-    theta_max = ts.a_theta[w] > theta_max ? ts.a_theta[w] : theta_max;
-    kmax = ts.a_kmax[w] > kmax ? ts.a_kmax[w] : kmax;
-    kmin = ts.a_kmin[w] < kmin ? ts.a_kmin[w] : kmin;
+  for (int q = 0; q < kRecPer; ++q) {
+    th_l = max(th_l, (uint32_t)(wr[q] >> 32));
+    km_l = max(km_l, (uint32_t)wr[q]);
   }
-  const bool all_kept = theta_max == kAllValid;
-  const bool exact = theta_max == ~0ull;
-  // 3. kept keys: at or above every wavefront threshold (with kAllValid,
-  // every valid key)
+  const uint32_t th_w = wave_reduce32(th_l, MaxOp{});
+  const bool exact = th_w == 0xffffffffu;
+  const uint64_t theta_max = exact ? ~0ull : (uint64_t)th_w << 32;
+  const uint64_t kmax = (uint64_t)wave_reduce32(km_l, MaxOp{}) << 32;
+  const bool all_kept = th_w == kMinValidOrd;
+  uint64_t kmin = 0;
+  if (all_kept) {
+    const uint64_t d = wave_min_u64(kmn);
+    if (lane == 0) ts.a_kmin[wave] = d;
+    __syncthreads();
+    kmin = ts.a_kmin[0];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) kmin = ts.a_kmin[w] < kmin ? ts.a_kmin[w] : kmin;
+  }
+  // 3. kept keys: at or above every wavefront threshold (when every
+  // wavefront kept all, every valid key)
   uint32_t vm = 0;
   const uint64_t (&yk)[kPer] = lk;
 #pragma unroll
