@@ -201,7 +201,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build samples on one GPU; multi-GPU runs are not part of it "
-              "(rows shard across GPUs with no communication, see DESIGN.md)", file=sys.stderr)
+              "(rows shard across GPUs with no communication)", file=sys.stderr)
         sys.exit(2)
 
     import torch
