@@ -1,8 +1,9 @@
-// Single-precision exp/ln/log2 that reproduce, bit for bit, the glibc >= 2.27
-// implementations that Rust's f32::{exp, ln, log2} lower to on x86_64-linux-gnu.
+// Single-precision exp/ln/log2/pow that reproduce, bit for bit, the glibc >= 2.27
+// implementations that Rust's f32::{exp, ln, log2, powf} lower to on
+// x86_64-linux-gnu.
 //
 // The reference sampler (crates/oxide-core/src/sampler.rs:289 exp, :424 and
-// :440/:451 log2, :496/:502 ln) calls the platform libm. glibc's single
+// :440/:451 log2, :496/:502 ln, :409 powf) calls the platform libm. glibc's single
 // precision routines are the published ARM optimized-routines algorithms
 // (Szabolcs Nagy, 2017; MIT licence): evaluate in double precision with a
 // 32-entry 2^(i/32) table (exp) or a 16-entry (1/c, log c) table (ln, log2) and
@@ -203,6 +204,109 @@ OXS_HD float log2f_t(float x, const double* invc_tab = kLogInvc, const double* l
   double p = mad<FUSED>(A3, r, y0);
   y = mad<FUSED>(y, r2, p);
   return (float)y;
+}
+
+// powf (the same published algorithm family): log2(x) in double from the
+// 16-entry (1/c, log2 c) table and a degree-5 polynomial, times y, then
+// exp2 of that from the 32-entry 2^(i/32) table and a cubic, rounded once.
+// Covers every input; the sampler calls it with finite exponents only.
+template <bool FUSED>
+OXS_HD double powf_log2(uint32_t ix, const double* invc_tab, const double* logc_tab) {
+  const double A0 = 0x1.27616c9496e0bp-2, A1 = -0x1.71969a075c67ap-2, A2 = 0x1.ec70a6ca7baddp-2,
+               A3 = -0x1.7154748bef6c8p-1, A4 = 0x1.71547652ab82bp0;
+  uint32_t tmp = ix - 0x3f330000u;
+  int i = (int)((tmp >> (23 - 4)) % 16);
+  uint32_t top = tmp & 0xff800000u;
+  uint32_t iz = ix - top;
+  int k = (int32_t)top >> 23;
+  double invc = invc_tab[i], logc = logc_tab[i];
+  double z = (double)u2f(iz);
+  double r = mad<FUSED>(z, invc, -1.0);
+  double y0 = logc + (double)k;
+  double r2 = r * r;
+  double y = mad<FUSED>(A0, r, A1);
+  double p = mad<FUSED>(A2, r, A3);
+  double r4 = r2 * r2;
+  double q = mad<FUSED>(A4, r, y0);
+  q = mad<FUSED>(p, r2, q);
+  y = mad<FUSED>(y, r4, q);
+  return y;
+}
+
+template <bool FUSED>
+OXS_HD double powf_exp2(double xd, uint64_t sign_bias, const uint64_t* exp2tab) {
+  const double kShift = 0x1.8p+52 / 32;
+  const double C0 = 0x1.c6af84b912394p-5, C1 = 0x1.ebfce50fac4f3p-3, C2 = 0x1.62e42ff0c52d6p-1;
+  double kd = xd + kShift;
+  uint64_t ki = d2u(kd);
+  kd -= kShift;
+  double r = xd - kd;
+  uint64_t t = exp2tab[ki % 32];
+  uint64_t ski = ki + sign_bias;
+  t += ski << (52 - 5);
+  double s = u2d(t);
+  double z = mad<FUSED>(C0, r, C1);
+  double r2 = r * r;
+  double y = mad<FUSED>(C2, r, 1.0);
+  y = mad<FUSED>(z, r2, y);
+  return y * s;
+}
+
+// 0 when y is not an integer, 1 when odd, 2 when even (y's bits iy).
+OXS_HD int powf_checkint(uint32_t iy) {
+  int e = (int)(iy >> 23 & 0xff);
+  if (e < 0x7f) return 0;
+  if (e > 0x7f + 23) return 2;
+  if (iy & ((1u << (0x7f + 23 - e)) - 1)) return 0;
+  if (iy & (1u << (0x7f + 23 - e))) return 1;
+  return 2;
+}
+
+OXS_HD bool powf_zeroinfnan(uint32_t ix) { return 2 * ix - 1 >= 2u * 0x7f800000u - 1; }
+OXS_HD bool powf_issignaling(uint32_t ix) { return 2 * (ix ^ 0x00400000u) > 2u * 0x7fc00000u; }
+
+template <bool FUSED>
+OXS_HD float powf_t(float x, float y, const uint64_t* exp2tab = kExp2Tab, const double* invc_tab = kLogInvc,
+                    const double* logc_tab = kLog2Logc) {
+  uint64_t sign_bias = 0;
+  uint32_t ix = f2u(x), iy = f2u(y);
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u || powf_zeroinfnan(iy)) {
+    // x is subnormal, negative, zero, inf or nan, or y is zero, inf or nan
+    if (powf_zeroinfnan(iy)) {
+      // a signalling nan operand still yields a nan where pow would give 1
+      if (2 * iy == 0) return powf_issignaling(ix) ? x + y : 1.0f;
+      if (ix == 0x3f800000u) return powf_issignaling(iy) ? x + y : 1.0f;
+      if (2 * ix > 2u * 0x7f800000u || 2 * iy > 2u * 0x7f800000u) return x + y;
+      if (2 * ix == 2 * 0x3f800000u) return 1.0f;
+      if ((2 * ix < 2 * 0x3f800000u) == !(iy & 0x80000000u)) return 0.0f;  // |x| < 1 && y == inf, or |x| > 1 && y == -inf
+      return y * y;
+    }
+    if (powf_zeroinfnan(ix)) {
+      float x2 = x * x;
+      if ((ix & 0x80000000u) && powf_checkint(iy) == 1) x2 = -x2;
+      return (iy & 0x80000000u) ? 1.0f / x2 : x2;
+    }
+    // x and y are non-zero finite
+    if (ix & 0x80000000u) {
+      int yint = powf_checkint(iy);
+      if (yint == 0) return u2f(0x7fc00000u);  // negative base, non-integer exponent
+      if (yint == 1) sign_bias = 1ull << (5 + 11);
+      ix &= 0x7fffffffu;
+    }
+    if (ix < 0x00800000u) {  // subnormal: normalise
+      ix = f2u(u2f(ix) * 0x1p23f);
+      ix &= 0x7fffffffu;
+      ix -= 23u << 23;
+    }
+  }
+  double logx = powf_log2<FUSED>(ix, invc_tab, logc_tab);
+  double ylogx = (double)y * logx;
+  if (((d2u(ylogx) >> 47) & 0xffff) >= (d2u(126.0) >> 47)) {
+    // |y * log2(x)| >= 126
+    if (ylogx > 0x1.fffffffd1d571p+6) return sign_bias ? -u2f(0x7f800000u) : u2f(0x7f800000u);  // overflow
+    if (ylogx <= -150.0) return sign_bias ? -0.0f : 0.0f;                                         // underflow
+  }
+  return (float)powf_exp2<FUSED>(ylogx, sign_bias, exp2tab);
 }
 
 }  // namespace oxs_libm

@@ -48,6 +48,8 @@ constexpr int kMaxChunk = 8192;   // logits per stream block
 constexpr int kMaxChunks = 64;    // chunks per row
 constexpr int kBuckets = 256;     // tail counting-sort buckets
 constexpr int kRecPer = kMaxChunks * kWavesPerBlock / 64;  // wavefront records per lane a tail wavefront reads
+constexpr int kDryMax = 1024;      // longest DRY history slice run on the device (sampler.rs:395)
+constexpr int kDryHash = 2048;     // DRY id hash slots
 constexpr int kHistUnroll = 4;    // history-window ids per stream thread read with the logits
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -56,6 +58,7 @@ constexpr uint32_t kCountMask = 0x0fffffffu;
 constexpr uint32_t kBanFlag = 1u << 28;
 constexpr uint32_t kBiasFlag = 1u << 29;
 constexpr uint32_t kNlFlag = 1u << 30;
+constexpr uint32_t kDryFlag = 1u << 31;  // exact-path table: the id has a DRY value
 
 struct Params {
   const void* logits;
@@ -94,6 +97,8 @@ struct Params {
   uint64_t* wave_theta;  // [B][S*4] wavefront records: threshold << 32 | largest key
   uint32_t* wave_count;  // [B][S*4]
   const uint64_t* libm;  // [kLibmWords]: the libm tables (exp2, 1/c, ln c, log2 c) as bit patterns
+  uint64_t* dry_list;    // [B][kDryMax]: DRY rows' (id << 32 | value bits), sorted by id
+  uint32_t* dry_count;   // [B]
 };
 
 // ---------------------------------------------------------------- keys
@@ -130,8 +135,8 @@ __device__ __forceinline__ uint32_t grouped_index(uint32_t block, uint32_t per_x
 // Per-row constants of the pre-softmax stages (sampler.rs:184-254).
 struct RowXf {
   bool pen_rep, pen_fp, use_hist, nl_active, any_special, do_temp, dry;
-  float rp, fp, pp, nl_pen, inv_temp;
-  uint32_t hlen, wstart, wn, nl_id;
+  float rp, fp, pp, nl_pen, inv_temp, dry_mult, dry_base;
+  uint32_t hlen, wstart, wn, nl_id, dry_allowed, dry_range;
   uint32_t bias_off, bias_cnt, ban_off, ban_cnt;
 };
 
@@ -157,37 +162,24 @@ __device__ __forceinline__ RowXf make_row_xf_h(const Params& p, const oxs_sampli
   r.bias_cnt = p.bias_ids ? c.bias_count : 0u;
   r.ban_off = c.ban_offset;
   r.ban_cnt = p.ban_ids ? c.ban_count : 0u;
-  r.any_special = r.use_hist || r.bias_cnt > 0 || r.ban_cnt > 0 || r.nl_active;
   r.do_temp = c.temperature > 0.0f && c.mirostat_mode == OXS_MIROSTAT_DISABLED;  // :249
   r.inv_temp = 1.0f / c.temperature;                                               // :250
   r.dry = c.dry_multiplier > 0.0f && hlen > 0;                                     // :203
+  r.dry_mult = c.dry_multiplier;
+  r.dry_base = c.dry_base;
+  r.dry_allowed = c.dry_allowed_length;
+  r.dry_range = c.dry_range;
+  r.any_special = r.use_hist || r.bias_cnt > 0 || r.ban_cnt > 0 || r.nl_active || r.dry;
   return r;
 }
 
 
 // The sparse pre-softmax stages for one marked logit, in reference order:
-// ban (:184-188), bias (:189-193), newline (:196-200), repetition (:217-229),
-// frequency/presence (:232-245). Temperature is applied by the caller.
-// The same stages with the id's bias value already found.
-__device__ __forceinline__ float apply_special_b(const RowXf& r, float x, uint32_t entry, float bias) {
-  if (entry & kBanFlag) x = neg_inf();
-  if (entry & kBiasFlag) x += bias;
-  if (entry & kNlFlag) x -= r.nl_pen;
-  const uint32_t cnt = entry & kCountMask;
-  if (cnt) {
-    if (r.pen_rep) x = (x > 0.0f) ? x / r.rp : x * r.rp;
-    if (r.pen_fp) {
-      const float t = (float)cnt * r.fp;
-      const float pen = t + r.pp;
-      x = x - pen;
-    }
-  }
-  return x;
-}
-
-__device__ __forceinline__ float apply_special(const uint32_t* bias_ids, const float* bias_values,
-                                               const RowXf& r, float x, uint32_t entry,
-                                               uint32_t idx) {
+// ban (:184-188), bias (:189-193), newline (:196-200), [DRY (:203-205)],
+// repetition (:217-229), frequency/presence (:232-245). Temperature is
+// applied by the caller.
+__device__ __forceinline__ float special_pre(const uint32_t* bias_ids, const float* bias_values, const RowXf& r,
+                                             float x, uint32_t entry, uint32_t idx) {
   if (entry & kBanFlag) x = neg_inf();
   if (entry & kBiasFlag) {
     float b = 0.0f;
@@ -196,6 +188,9 @@ __device__ __forceinline__ float apply_special(const uint32_t* bias_ids, const f
     x += b;
   }
   if (entry & kNlFlag) x -= r.nl_pen;
+  return x;
+}
+__device__ __forceinline__ float special_post(const RowXf& r, float x, uint32_t entry) {
   const uint32_t cnt = entry & kCountMask;
   if (cnt) {
     if (r.pen_rep) x = (x > 0.0f) ? x / r.rp : x * r.rp;
@@ -206,6 +201,11 @@ __device__ __forceinline__ float apply_special(const uint32_t* bias_ids, const f
     }
   }
   return x;
+}
+__device__ __forceinline__ float apply_special(const uint32_t* bias_ids, const float* bias_values,
+                                               const RowXf& r, float x, uint32_t entry,
+                                               uint32_t idx) {
+  return special_post(r, special_pre(bias_ids, bias_values, r, x, entry, idx), entry);
 }
 
 template <int DT>
@@ -791,7 +791,27 @@ __device__ __forceinline__ void build_table(const Params& p, const RowXf& r, uin
     if (id >= c0 && id < c1) atomicOr(&table[id - c0], kBiasFlag);
   }
   if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1) atomicOr(&table[r.nl_id - c0], kNlFlag);
+  if (r.dry) {
+    const uint64_t* dl = p.dry_list + (size_t)row * kDryMax;
+    const uint32_t nd = p.dry_count[row];
+    for (uint32_t k = tid; k < nd; k += kThreads) {
+      const uint32_t id = (uint32_t)(dl[k] >> 32);
+      if (id >= c0 && id < c1) atomicOr(&table[id - c0], kDryFlag);
+    }
+  }
   __syncthreads();
+}
+
+// The DRY-stage value of id (the row's sorted DRY list holds it).
+__device__ __forceinline__ float dry_value(const Params& p, uint32_t row, uint32_t id) {
+  const uint64_t* dl = p.dry_list + (size_t)row * kDryMax;
+  uint32_t lo = 0, hi = p.dry_count[row];
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if ((uint32_t)(dl[mid] >> 32) <= id) lo = mid;
+    else hi = mid;
+  }
+  return __uint_as_float((uint32_t)dl[lo]);
 }
 
 template <int DT>
@@ -802,7 +822,8 @@ __device__ __forceinline__ float transformed_logit(const Params& p, const RowXf&
   if (p.mask && !mask_allows(p, row, idx)) x = neg_inf();
   if (r.any_special) {
     const uint32_t e = table[idx - c0];
-    if (e) x = apply_special(p.bias_ids, p.bias_values, r, x, e, idx);
+    if (e & kDryFlag) x = special_post(r, dry_value(p, row, idx), e);  // mask, ban, bias, newline, DRY included
+    else if (e) x = apply_special(p.bias_ids, p.bias_values, r, x, e, idx);
   }
   if (r.do_temp) x *= r.inv_temp;
   return x;
@@ -829,7 +850,11 @@ __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowX
       const uint32_t c1 = min(c0 + p.CH, p.V);
       if (r.any_special) build_table(p, r, row, c0, c1, table);
       for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
-        const uint32_t k = cand_key(transformed_logit<DT>(p, r, row, i, c0, table));
+        const float y = transformed_logit<DT>(p, r, row, i, c0, table);
+        // the stream kernel's write-back has no DRY: the DRY ids' values here
+        if (d == 0 && r.dry && p.logits_out && (table[i - c0] & kDryFlag))
+          p.logits_out[(size_t)row * p.logits_out_ld + i] = y;
+        const uint32_t k = cand_key(y);
         if (!k) continue;
         const uint64_t key = comp_key(k, i);
         if ((key & mask) == prefix) atomicAdd(&hist[(uint32_t)(key >> shift) & 255u], 1u);
@@ -1372,6 +1397,104 @@ __device__ uint32_t sort_select(const uint64_t (&lk)[kPer], uint32_t vm, uint32_
   return n;
 }
 
+// ---------------------------------------------------------------- DRY
+
+__device__ __forceinline__ float dpowf(float x, float y, const LibmTables& t) {
+  return oxs_libm::powf_t<true>(x, y, t.exp2, t.invc, t.log2c);
+}
+
+// Ban (:184-188), bias (:189-193) and newline (:196-200) for one id, found in
+// the row's lists.
+__device__ __forceinline__ float pre_stages_of(const Params& p, const RowXf& r, uint32_t id, float x) {
+  uint32_t e = 0;
+  for (uint32_t k = 0; k < r.ban_cnt; ++k)
+    if (p.ban_ids[r.ban_off + k] == id) e |= kBanFlag;
+  for (uint32_t k = 0; k < r.bias_cnt; ++k)
+    if (p.bias_ids[r.bias_off + k] == id) e |= kBiasFlag;
+  if (r.nl_active && id == r.nl_id) e |= kNlFlag;
+  return special_pre(p.bias_ids, p.bias_values, r, x, e, id);
+}
+
+// DRY (sampler.rs:393-415) for one row, by its tail block. Over the last
+// dry_range history ids, for match lengths 32 down to allowed_length, every
+// earlier position whose n-gram equals the slice's suffix penalises the id
+// after it by multiplier * base^(length - allowed_length). An id's value starts
+// at its logit after the mask, bans, biases and newline, and takes its
+// penalties one rounded subtraction at a time in the reference's order
+// (longer matches first; the penalties of one length are equal, so their order
+// inside a length does not matter). The ids and values go to the row's list,
+// sorted by id. Uses the first 28 KB of `lds`.
+template <int DT>
+__device__ __forceinline__ void dry_pass(const Params& p, const RowXf& r, uint32_t row, uint32_t* lds,
+                                         const LibmTables& tab, TailShared& ts) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t L = min(r.hlen, r.dry_range);  // :394-396; the caller checked L <= kDryMax
+  uint32_t* slice = lds;                         // [kDryMax]
+  uint32_t* hkey = slice + kDryMax;              // [kDryHash] ids (kEmptySlot: free)
+  uint32_t* cnt = hkey + kDryHash;               // [kDryHash] matches at the current length
+  float* val = (float*)(cnt + kDryHash);         // [kDryHash] values
+  const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
+  for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
+  for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+    hkey[h] = kEmptySlot;
+    cnt[h] = 0;
+  }
+  __syncthreads();
+  const int allowed = (int)min(r.dry_allowed, 33u);
+  for (int ml = 32; ml >= allowed; --ml) {  // (allowed..=32).rev()
+    if (L < (uint32_t)ml) continue;         // :399-401
+    const uint32_t n = L - (uint32_t)ml;
+    for (uint32_t i = tid; i < n; i += kThreads) {
+      bool m = true;
+      for (int t = 0; t < ml && m; ++t) m = slice[i + t] == slice[L - ml + t];
+      if (!m) continue;
+      const uint32_t next = slice[i + ml];
+      if (next >= p.V) continue;  // logits.get_mut(next) is None
+      uint32_t h = (next * 0x9e3779b1u) >> 21;
+      for (int probe = 0; probe < kDryHash; ++probe) {  // at most L <= kDryHash / 2 distinct ids
+        const uint32_t prev = atomicCAS(&hkey[h], kEmptySlot, next);
+        if (prev == kEmptySlot) {  // first sight: the value before DRY
+          float x = load_logit<DT>(p, row, next);
+          if (p.mask && !mask_allows(p, row, next)) x = neg_inf();
+          val[h] = pre_stages_of(p, r, next, x);
+        }
+        if (prev == kEmptySlot || prev == next) {
+          atomicAdd(&cnt[h], 1u);
+          break;
+        }
+        h = (h + 1) & (kDryHash - 1);
+      }
+    }
+    __syncthreads();
+    const float exponent = (float)(ml - allowed);
+    const float pen = r.dry_mult * dpowf(r.dry_base, exponent, tab);  // :408-409
+    for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+      const uint32_t k = cnt[h];
+      if (k) {
+        float v = val[h];
+        for (uint32_t j = 0; j < k; ++j) v = v - pen;  // :411
+        val[h] = v;
+        cnt[h] = 0;
+      }
+    }
+    __syncthreads();
+  }
+  uint64_t* keys = (uint64_t*)cnt;  // [kDryMax] (id << 32 | value bits), in the cleared counters
+  if (tid == 0) ts.counter = 0;
+  __syncthreads();
+  for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+    const uint32_t id = hkey[h];
+    if (id != kEmptySlot) keys[atomicAdd(&ts.counter, 1u)] = ((uint64_t)id << 32) | __float_as_uint(val[h]);
+  }
+  __syncthreads();
+  const uint32_t nd = ts.counter;
+  bitonic_sort<true>(keys, nd);
+  uint64_t* dl = p.dry_list + (size_t)row * kDryMax;
+  for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = keys[i];
+  if (tid == 0) p.dry_count[row] = nd;
+  __syncthreads();
+}
+
 // ---------------------------------------------------------------- tail kernel
 
 // ids / exps of sorted keys[0..n) (n >= 1) into the chain arrays; ends with a barrier.
@@ -1446,14 +1569,17 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
 
 
   const uint32_t M = max(c.top_k, 256u);
-  if (r.dry || M > (uint32_t)kMaxM) {  // stages this build does not run on the device
-    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED);
+  if (M > (uint32_t)kMaxM || (r.dry && min(r.hlen, r.dry_range) > (uint32_t)kDryMax)) {
+    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED);  // sizes this build does not run on the device
     return;
   }
   if (c.mirostat_mode != OXS_MIROSTAT_DISABLED && !p.mu) {
     write_row_result(p, row, 0u, OXS_ROW_MISSING_STATE);
     return;
   }
+  // DRY rows: their values, then the exact path (the stream kernel's
+  // candidates do not include DRY)
+  if (r.dry) dry_pass<DT>(p, r, row, (uint32_t*)s_keys, s_tab, ts);
 
   // 2. the largest wavefront threshold and the largest key, from the
   // wavefront records, reduced by every wavefront on its own (a record of all
@@ -1478,7 +1604,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     km_l = max(km_l, (uint32_t)wr[q]);
   }
   const uint32_t th_w = wave_reduce32(th_l, MaxOp{});
-  const bool exact = th_w == 0xffffffffu;
+  const bool exact = th_w == 0xffffffffu || r.dry;
   const uint64_t theta_max = exact ? ~0ull : (uint64_t)th_w << 32;
   const uint64_t kmax = (uint64_t)wave_reduce32(km_l, MaxOp{}) << 32;
   const bool all_kept = th_w == kMinValidOrd;
@@ -1700,6 +1826,8 @@ struct oxs_sampler {
   uint64_t* wave_theta;
   uint32_t* wave_count;
   uint64_t* libm;
+  uint64_t* dry_list;
+  uint32_t* dry_count;
   size_t bytes;
 };
 
@@ -1777,8 +1905,11 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
   bool ok = hipMalloc((void**)&s->lists, b_lists) == hipSuccess &&
                   hipMalloc((void**)&s->wave_theta, b_theta) == hipSuccess &&
                   hipMalloc((void**)&s->wave_count, b_count) == hipSuccess &&
-                  hipMalloc((void**)&s->libm, oxs::kLibmWords * sizeof(uint64_t)) == hipSuccess;
-  s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t);
+                  hipMalloc((void**)&s->libm, oxs::kLibmWords * sizeof(uint64_t)) == hipSuccess &&
+                  hipMalloc((void**)&s->dry_list, B * oxs::kDryMax * sizeof(uint64_t)) == hipSuccess &&
+                  hipMalloc((void**)&s->dry_count, B * sizeof(uint32_t)) == hipSuccess;
+  s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t) +
+             B * (oxs::kDryMax * sizeof(uint64_t) + sizeof(uint32_t));
   if (ok) {  // the libm tables, as bit patterns, in the workspace
     uint64_t host[oxs::kLibmWords];
     ok = hipMemcpyFromSymbol(host, HIP_SYMBOL(oxs_libm::kExp2Tab), 32 * sizeof(uint64_t)) == hipSuccess &&
@@ -1801,6 +1932,8 @@ int oxs_sampler_destroy(oxs_sampler* s) {
   if (s->wave_theta) (void)hipFree(s->wave_theta);
   if (s->wave_count) (void)hipFree(s->wave_count);
   if (s->libm) (void)hipFree(s->libm);
+  if (s->dry_list) (void)hipFree(s->dry_list);
+  if (s->dry_count) (void)hipFree(s->dry_count);
   free(s);
   return OXS_OK;
 }
@@ -1873,6 +2006,8 @@ int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
   p.wave_theta = s->wave_theta;
   p.wave_count = s->wave_count;
   p.libm = s->libm;
+  p.dry_list = s->dry_list;
+  p.dry_count = s->dry_count;
   // Group rows by XCD when the batch divides evenly over the 8 XCDs.
   p.rpx = (b->batch % 8 == 0) ? b->batch / 8 : 0;
   const uint32_t epl = b->logits_dtype == OXS_DTYPE_F32 ? 4 : 8;

@@ -1,5 +1,5 @@
 // Sweeps the device libm emulation (oxs_libm.h, compiled here as host C++)
-// against the host's glibc expf/logf/log2f, bit for bit.
+// against the host's glibc expf/logf/log2f/powf, bit for bit.
 //
 // usage: libm_sweep FUSED STRIDE
 //   FUSED  1 compares the fused-multiply-add form (what glibc's ifunc picks on
@@ -50,10 +50,23 @@ int run(uint64_t stride) {
     tl.add(b, same(logf_t<FUSED>(x), logf(x)));
     t2.add(b, same(log2f_t<FUSED>(x), log2f(x)));
   }
+  // powf: every stride-th base with the integer exponents DRY uses (0..40),
+  // plus bases and exponents from the same sweep
+  Tally tp;
+  for (uint64_t b = 0; b <= 0xffffffffull; b += stride * 64) {
+    const float x = u2f((uint32_t)b);
+    for (int e = 0; e <= 40; ++e) {
+      const float y = (float)e;
+      tp.add((uint32_t)b, same(powf_t<FUSED>(x, y), powf(x, y)));
+    }
+    const float y2 = u2f((uint32_t)(b * 2654435761ull));
+    tp.add((uint32_t)b, same(powf_t<FUSED>(x, y2), powf(x, y2)));
+  }
   printf("expf %llu %llu %08x\n", te.checked, te.bad, te.first);
+  printf("powf %llu %llu %08x\n", tp.checked, tp.bad, tp.first);
   printf("logf %llu %llu %08x\n", tl.checked, tl.bad, tl.first);
   printf("log2f %llu %llu %08x\n", t2.checked, t2.bad, t2.first);
-  return (te.bad | tl.bad | t2.bad) ? 1 : 0;
+  return (te.bad | tl.bad | t2.bad | tp.bad) ? 1 : 0;
 }
 
 }  // namespace

@@ -45,11 +45,7 @@ def test_academic_sampler_min_p_and_xtc(backend):
     assert sampler.sample_token(logits, state, 13) == 1
 
 
-@pytest.mark.parametrize("backend", [
-    pytest.param("oracle", id="oracle"),
-    pytest.param("gpu", id="gpu", marks=[pytest.mark.gpu, pytest.mark.skip(
-        reason="DRY (sampler.rs:393-415) is not yet run on the device; such rows return OXS_ROW_UNSUPPORTED")]),
-])
+@pytest.mark.parametrize("backend", BACKENDS)
 def test_dry_repetition_penalty(backend):
     # academic_samplers_test.rs:39-56
     logits = [5.0, 5.0, 5.0]

@@ -99,6 +99,12 @@ def mixed_workload(B, V, seed):
         SamplingConfig(),
         wl.disabled_config(temperature=0.6, frequency_penalty=-0.5, presence_penalty=-0.2, repeat_penalty=0.8,
                            repeat_last_n=0),
+        # DRY (sampler.rs:393-415) with the other sparse stages, and with allowed_length 0
+        wl.disabled_config(temperature=0.8, dry_multiplier=0.8, dry_base=1.75, dry_allowed_length=2, dry_range=64,
+                           repeat_penalty=1.1, repeat_last_n=16, logit_biases={7 % V: 2.0}, banned_tokens={3 % V},
+                           penalize_nl=True),
+        wl.disabled_config(temperature=1.0, dry_multiplier=1.5, dry_base=1.1, dry_allowed_length=0, dry_range=300,
+                           top_k=30),
     ]
     configs = [base[i % len(base)] for i in range(B)]
     cap = 300
@@ -106,6 +112,10 @@ def mixed_workload(B, V, seed):
     history[:, ::7] = np.uint32(min(10, V - 1))  # the newline id recurs
     hlen = rng.integers(0, 200, size=B).astype(np.uint32)
     hlen[min(5, B - 1)] = cap  # no room to record: OXS_ROW_HISTORY_FULL
+    for b in range(B):  # a repeated motif at the end of each history: n-gram matches for DRY
+        n = int(hlen[b])
+        if n >= 40:
+            history[b, n - 40:n] = np.tile(rng.integers(0, V, size=5, dtype=np.uint32), 8)
     if B > 13:
         logits[13, :] = -np.inf  # OXS_ROW_EMPTY
     mu = np.full(B, 10.0, np.float32)
