@@ -211,6 +211,44 @@ size_t oxs_sampler_workspace_bytes(const oxs_sampler* sampler);
  */
 int oxs_sample_batch(oxs_sampler* sampler, const oxs_batch* batch, void* stream);
 
+/*
+ * Grammar masks from a DFA (the producer of oxs_batch.allowed_mask).
+ *
+ * DfaSchemaGrammar (crates/oxide-core/src/dfa.rs:4-148): a transition table of
+ * num_states x 256 next states, OXS_DFA_ERROR_STATE meaning "no transition".
+ * For every row b and token t < vocab, bit (t % 32) of word t / 32 of row b's
+ * mask is set when the token's bytes walk the table from states[b] without an
+ * error: every step needs a current state < num_states and a next state other
+ * than OXS_DFA_ERROR_STATE (DfaSchemaGrammar::transition, dfa.rs:110-126). A
+ * token with no bytes is allowed. This is compute_token_mask
+ * (crates/oxide-server/src/grammar_engine.rs:42-65) and the -inf pattern of
+ * apply_dfa_mask (dfa.rs:130-148) for a batch of rows, as a packed bitmask:
+ * bits past vocab in the last word are cleared; words past ceil(vocab / 32)
+ * are not written.
+ */
+#define OXS_DFA_ERROR_STATE 0xffffffffu
+
+typedef struct oxs_dfa {
+  uint32_t num_states;
+  const uint32_t* transitions; /* [num_states][256], device */
+} oxs_dfa;
+
+typedef struct oxs_token_bytes {
+  uint32_t vocab;
+  uint32_t num_bytes;      /* bytes in `bytes`; a token whose range is not inside it is not allowed */
+  const uint32_t* offsets; /* [vocab + 1]: token t is bytes[offsets[t] .. offsets[t + 1]), device */
+  const uint8_t* bytes;    /* device */
+} oxs_token_bytes;
+
+/*
+ * Writes mask[b * mask_ld + w] for b < batch, w < ceil(vocab / 32), from
+ * states[b] (device [batch]). Asynchronous on `stream`; allocates nothing.
+ * Returns OXS_ERR_INVALID_ARGUMENT for missing pointers, mask_ld too small,
+ * vocab above 2^31 or batch above 1048560, OXS_ERR_HIP if the launch fails.
+ */
+int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, const uint32_t* states, uint32_t batch,
+                 uint32_t* mask, int64_t mask_ld, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

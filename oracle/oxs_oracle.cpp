@@ -429,3 +429,29 @@ float oxo_log2f(float x) { return log2f(x); }
 float oxo_powf(float x, float y) { return powf(x, y); }
 
 }  // extern "C"
+
+// grammar_engine.rs:42-65 / dfa.rs:110-148: walk each token's bytes from the
+// row's state; DfaSchemaGrammar::transition fails for a current state outside
+// the table (:111-116) or an error entry (:119-124).
+void oxo_dfa_mask(const uint32_t* transitions, uint32_t num_states, const uint32_t* offsets,
+                  const uint8_t* bytes, uint32_t num_bytes, uint32_t vocab, const uint32_t* states,
+                  uint32_t batch, uint32_t* mask, int64_t mask_ld) {
+  const uint32_t words = (vocab + 31) / 32;
+  for (uint32_t b = 0; b < batch; ++b) {
+    uint32_t* row = mask + (size_t)b * mask_ld;
+    for (uint32_t w = 0; w < words; ++w) row[w] = 0;
+    for (uint32_t t = 0; t < vocab; ++t) {
+      const uint32_t lo = offsets[t], hi = offsets[t + 1];
+      if (hi < lo || hi > num_bytes) continue;
+      uint32_t state = states[b];
+      bool valid = true;
+      for (uint32_t i = lo; i < hi; ++i) {
+        if (state >= num_states) { valid = false; break; }
+        const uint32_t next = transitions[(size_t)state * 256 + bytes[i]];
+        if (next == 0xffffffffu) { valid = false; break; }
+        state = next;
+      }
+      if (valid) row[t / 32] |= 1u << (t % 32);
+    }
+  }
+}

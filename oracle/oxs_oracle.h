@@ -64,6 +64,18 @@ int oxo_sample_token(const oxs_sampling_config* cfg, const uint32_t* bias_ids,
  */
 int oxo_sample_batch(const oxs_batch* batch, int n_threads);
 
+/*
+ * StructuredOutputEngine::compute_token_mask (oxide-server/src/grammar_engine.rs:42-65),
+ * equivalently the -inf pattern of DfaSchemaGrammar::apply_dfa_mask
+ * (oxide-core/src/dfa.rs:130-148), for `batch` rows in states[b], as the packed
+ * mask oxs_dfa_mask writes (bit t % 32 of word t / 32 set = token t allowed;
+ * bits past vocab cleared). Host pointers. Token t is bytes[offsets[t] ..
+ * offsets[t + 1]); a range outside [0, num_bytes) is not allowed.
+ */
+void oxo_dfa_mask(const uint32_t* transitions, uint32_t num_states, const uint32_t* offsets,
+                  const uint8_t* bytes, uint32_t num_bytes, uint32_t vocab, const uint32_t* states,
+                  uint32_t batch, uint32_t* mask, int64_t mask_ld);
+
 /* glibc's expf etc., exported so tests can compare the device emulation. */
 float oxo_expf(float x);
 float oxo_logf(float x);

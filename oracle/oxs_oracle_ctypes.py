@@ -50,6 +50,9 @@ def load() -> ctypes.CDLL:
         getattr(lib, f).argtypes = [ctypes.c_float]
     lib.oxo_powf.restype = ctypes.c_float
     lib.oxo_powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    lib.oxo_dfa_mask.restype = None
+    lib.oxo_dfa_mask.argtypes = [vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32,
+                                 vp, ctypes.c_int64]
     _lib = lib
     return lib
 
@@ -153,3 +156,19 @@ class OracleEngine:
         n = min(int(kc[0]), kept_cap)
         state.candidates_buffer = [(int(i), float(p)) for i, p in zip(kids[:n], kp[:n])]
         return int(tok[0])
+
+
+def dfa_mask_host(transitions, num_states, offsets, byte_arr, states):
+    """The oracle's packed grammar masks: [batch, ceil(vocab / 32)] uint32."""
+    lib = load()
+    transitions = np.ascontiguousarray(transitions, dtype=np.uint32)
+    offsets = np.ascontiguousarray(offsets, dtype=np.uint32)
+    byte_arr = np.ascontiguousarray(byte_arr, dtype=np.uint8)
+    states = np.ascontiguousarray(states, dtype=np.uint32)
+    vocab = offsets.shape[0] - 1
+    words = (vocab + 31) // 32
+    mask = np.zeros((states.shape[0], max(words, 1)), np.uint32)
+    lib.oxo_dfa_mask(_ptr(transitions) if transitions.size else None, num_states, _ptr(offsets),
+                     _ptr(byte_arr) if byte_arr.size else None, byte_arr.shape[0], vocab, _ptr(states),
+                     states.shape[0], _ptr(mask), mask.shape[1])
+    return mask[:, :words]

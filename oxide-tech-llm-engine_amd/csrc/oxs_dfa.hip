@@ -1,0 +1,151 @@
+// oxs_dfa.hip — grammar masks from a DFA for MI355X (gfx950).
+//
+// For a batch of rows, each in its own DFA state, walks every vocabulary
+// token's bytes through the transition table (crates/oxide-core/src/dfa.rs:110-148,
+// crates/oxide-server/src/grammar_engine.rs:42-65) and writes the packed
+// allowed-token bitmask that oxs_sample_batch reads (oxs_batch.allowed_mask).
+//
+// One thread per token: its first kMaxBytes bytes are read once into registers
+// and walked for every row of the block's row group, four rows at a time so
+// that four independent table reads are in flight per step. The table sits in
+// LDS when it fits. A walk is a chain of dependent table reads, so the table
+// lookups bound this kernel, not HBM (the token bytes and offsets are read once
+// per row group). A wavefront's 64 consecutive tokens give two mask words per
+// row from one ballot.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/oxide_sampler.h"
+
+namespace oxs_grammar {
+
+constexpr int kThreads = 256;
+constexpr int kTokPerThread = 4;      // tokens per thread (amortises the table's load into LDS)
+constexpr int kRowsPerBlock = 16;     // rows walked per block
+constexpr int kRowIlp = 4;            // rows walked together
+constexpr int kMaxBytes = 16;         // bytes held in registers; longer tokens read the rest from memory
+constexpr uint32_t kLdsStates = 48;   // tables of up to 48 states (48 KB) are copied into LDS
+constexpr uint32_t kErr = OXS_DFA_ERROR_STATE;
+static_assert(kRowsPerBlock % kRowIlp == 0, "row groups are walked kRowIlp at a time");
+
+struct Params {
+  const uint32_t* trans;
+  uint32_t num_states;
+  const uint32_t* offsets;
+  const uint8_t* bytes;
+  uint32_t num_bytes;
+  uint32_t V;
+  const uint32_t* states;
+  uint32_t B;
+  uint32_t* mask;
+  int64_t mask_ld;
+};
+
+// One transition (DfaSchemaGrammar::transition, dfa.rs:110-126): a current
+// state outside the table or an error entry ends the walk as invalid.
+__device__ __forceinline__ void step(const uint32_t* T, uint32_t ns, uint32_t byte, uint32_t& s, bool& ok) {
+  if (!ok) return;
+  if (s >= ns) {
+    ok = false;
+    return;
+  }
+  s = T[s * 256u + byte];
+  ok = s != kErr;
+}
+
+template <bool LDS>
+__global__ __launch_bounds__(kThreads) void dfa_mask_kernel(const Params p) {
+  extern __shared__ __align__(16) uint32_t s_trans[];  // [num_states * 256] with LDS
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  if (LDS) {
+    const uint32_t n4 = p.num_states * 64u;  // 16-byte groups
+    for (uint32_t i = tid; i < n4; i += kThreads) ((uint4*)s_trans)[i] = ((const uint4*)p.trans)[i];
+    __syncthreads();
+  }
+  const uint32_t* T = LDS ? s_trans : p.trans;
+  const uint32_t ns = p.num_states;
+  const uint32_t r0 = blockIdx.y * kRowsPerBlock;
+  const uint32_t nr = min((uint32_t)kRowsPerBlock, p.B - r0);
+  const uint32_t words = (p.V + 31u) / 32u;
+  for (int k = 0; k < kTokPerThread; ++k) {
+    // consecutive tokens per wavefront, the wavefront's first one 64-aligned
+    const uint32_t t = (blockIdx.x * kTokPerThread + k) * kThreads + tid;
+    bool in = t < p.V;
+    uint32_t b0 = 0, len = 0;
+    if (in) {
+      b0 = p.offsets[t];
+      const uint32_t e = p.offsets[t + 1];
+      if (e >= b0 && e <= p.num_bytes) len = e - b0;
+      else in = false;  // a range outside the byte array: not allowed, nothing read
+    }
+    uint32_t by[kMaxBytes];
+#pragma unroll
+    for (int j = 0; j < kMaxBytes; ++j) by[j] = (uint32_t)j < len ? p.bytes[b0 + j] : 0u;
+    const uint32_t wbase = (t - lane) / 32u;  // the wavefront's first mask word
+    for (uint32_t r = 0; r < nr; r += kRowIlp) {
+      uint32_t s[kRowIlp];
+      bool ok[kRowIlp];
+#pragma unroll
+      for (int q = 0; q < kRowIlp; ++q) {
+        const bool live = r + q < nr;
+        s[q] = p.states[r0 + (live ? r + q : 0u)];
+        ok[q] = in && live;
+      }
+#pragma unroll
+      for (int j = 0; j < kMaxBytes; ++j) {
+        if ((uint32_t)j < len) {
+#pragma unroll
+          for (int q = 0; q < kRowIlp; ++q) step(T, ns, by[j], s[q], ok[q]);
+        }
+      }
+      for (uint32_t j = kMaxBytes; j < len; ++j) {  // tokens longer than kMaxBytes
+        const uint32_t b = p.bytes[b0 + j];
+#pragma unroll
+        for (int q = 0; q < kRowIlp; ++q) step(T, ns, b, s[q], ok[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < kRowIlp; ++q) {
+        const uint64_t m = __ballot(ok[q]);
+        if (r + q < nr) {
+          uint32_t* row = p.mask + (size_t)(r0 + r + q) * p.mask_ld;
+          if (lane == 0 && wbase < words) row[wbase] = (uint32_t)m;
+          if (lane == 32 && wbase + 1 < words) row[wbase + 1] = (uint32_t)(m >> 32);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace oxs_grammar
+
+extern "C" int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, const uint32_t* states,
+                            uint32_t batch, uint32_t* mask, int64_t mask_ld, void* stream) {
+  using namespace oxs_grammar;
+  if (!dfa || !tokens) return OXS_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || tokens->vocab == 0) return OXS_OK;
+  if ((dfa->num_states && !dfa->transitions) || !tokens->offsets || !tokens->bytes || !states || !mask)
+    return OXS_ERR_INVALID_ARGUMENT;
+  if (mask_ld < (int64_t)((tokens->vocab + 31u) / 32u)) return OXS_ERR_INVALID_ARGUMENT;
+  // token indices stay below 2^31 and row groups within the grid's y extent
+  if (tokens->vocab > (1u << 31) || batch > 65535u * kRowsPerBlock) return OXS_ERR_INVALID_ARGUMENT;
+  Params p;
+  p.trans = dfa->transitions;
+  p.num_states = dfa->num_states;
+  p.offsets = tokens->offsets;
+  p.bytes = tokens->bytes;
+  p.num_bytes = tokens->num_bytes;
+  p.V = tokens->vocab;
+  p.states = states;
+  p.B = batch;
+  p.mask = mask;
+  p.mask_ld = mask_ld;
+  const uint32_t per_block = (uint32_t)(kThreads * kTokPerThread);
+  const dim3 grid((p.V + per_block - 1) / per_block, (batch + kRowsPerBlock - 1) / kRowsPerBlock);
+  hipStream_t st = (hipStream_t)stream;
+  // the table is copied into LDS in 16-byte pieces: small and 16-byte aligned tables only
+  if (p.num_states <= kLdsStates && ((uintptr_t)p.trans & 15u) == 0)
+    hipLaunchKernelGGL(dfa_mask_kernel<true>, grid, dim3(kThreads), p.num_states * 256u * sizeof(uint32_t), st, p);
+  else
+    hipLaunchKernelGGL(dfa_mask_kernel<false>, grid, dim3(kThreads), 0, st, p);
+  return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+}

@@ -1,12 +1,14 @@
 """Python view of the MI355X batched token sampler (liboxide_sampler.so).
 
-Two layers, both thin over the C ABI in include/oxide_sampler.h:
+Three layers, all thin over the C ABI in include/oxide_sampler.h:
 
 - `BatchSampler`: the batched device call, `oxs_sample_batch`, on torch
   tensors that already live on the GPU (the decode-loop form).
 - `SamplingConfig`, `MirostatMode`, `SamplerState`, `AcademicSamplerEngine`:
   the reference's single-row API (crates/oxide-core/src/sampler.rs:15-390),
   same names and argument meaning, each call running one row on the GPU.
+- `DfaSchemaGrammar`: the reference's grammar DFA (crates/oxide-core/src/dfa.rs),
+  whose token masks run on the GPU (`oxs_dfa_mask`) and feed the sampler.
 
 There is no CPU path: without the built library every call raises
 `LibraryMissing`.
@@ -20,6 +22,7 @@ from .engine import (
     ShapeMismatch,
     configs_to_array,
 )
+from .grammar import DfaSchemaGrammar, SchemaMismatch, TokenBytes
 from ._abi import (
     LibraryMissing,
     OxsError,
@@ -34,6 +37,9 @@ __all__ = [
     "SamplingConfig",
     "ShapeMismatch",
     "configs_to_array",
+    "DfaSchemaGrammar",
+    "SchemaMismatch",
+    "TokenBytes",
     "LibraryMissing",
     "OxsError",
     "load_library",

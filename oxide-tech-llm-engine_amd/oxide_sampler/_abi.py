@@ -49,7 +49,10 @@ EXPORTED_SYMBOLS = (
     "oxs_sampler_destroy",
     "oxs_sampler_workspace_bytes",
     "oxs_sample_batch",
+    "oxs_dfa_mask",
 )
+
+OXS_DFA_ERROR_STATE = 0xFFFFFFFF
 
 
 class OxsSamplingConfig(ctypes.Structure):
@@ -123,6 +126,22 @@ class OxsBatch(ctypes.Structure):
     ]
 
 
+class OxsDfa(ctypes.Structure):
+    _fields_ = [
+        ("num_states", ctypes.c_uint32),
+        ("transitions", ctypes.c_void_p),
+    ]
+
+
+class OxsTokenBytes(ctypes.Structure):
+    _fields_ = [
+        ("vocab", ctypes.c_uint32),
+        ("num_bytes", ctypes.c_uint32),
+        ("offsets", ctypes.c_void_p),
+        ("bytes", ctypes.c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -159,6 +178,9 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_sampler_workspace_bytes.argtypes = [ctypes.c_void_p]
     lib.oxs_sample_batch.restype = ctypes.c_int
     lib.oxs_sample_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.c_void_p]
+    lib.oxs_dfa_mask.restype = ctypes.c_int
+    lib.oxs_dfa_mask.argtypes = [ctypes.POINTER(OxsDfa), ctypes.POINTER(OxsTokenBytes), ctypes.c_void_p,
+                                 ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     if lib.oxs_abi_version() != OXS_ABI_VERSION:
         raise RuntimeError(f"liboxide_sampler ABI {lib.oxs_abi_version()} != {OXS_ABI_VERSION}")
     if path is None:

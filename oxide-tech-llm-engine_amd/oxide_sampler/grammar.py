@@ -1,0 +1,191 @@
+"""The reference's DFA grammar API over the GPU mask kernel.
+
+`DfaSchemaGrammar` keeps the names, constructors and behaviour of
+crates/oxide-core/src/dfa.rs:4-190 (the same type is re-exported by
+crates/oxide-server/src/dfa.rs). Its token masks run on the GPU through
+`oxs_dfa_mask` (the C ABI in include/oxide_sampler.h):
+
+- `DfaSchemaGrammar.token_masks(token_bytes, states)`: packed allowed-token
+  masks for a batch of rows, ready for `oxs_sample_batch`'s allowed_mask
+  (StructuredOutputEngine::compute_token_mask, grammar_engine.rs:42-65);
+- `DfaSchemaGrammar.apply_dfa_mask(state, vocab_bytes, logits)`: the reference's
+  in-place -inf masking of one row (dfa.rs:130-148).
+
+`transition`, `deterministic_transition` and `find_jump_forward_bytes` walk the
+table on the host, as the reference does (dfa.rs:110-190): they are single
+lookups, not a data-parallel path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from . import _abi
+from ._abi import OxsDfa, OxsTokenBytes, check, load_library
+
+DFA_ERROR_STATE = _abi.OXS_DFA_ERROR_STATE
+
+
+class SchemaMismatch(ValueError):
+    """EngineError::SchemaMismatch { state, byte } (crates/oxide-core/src/error.rs)."""
+
+    def __init__(self, state: int, byte: int):
+        super().__init__(f"schema mismatch at state {state}, byte {byte}")
+        self.state = state
+        self.byte = byte
+
+
+def _torch():
+    import torch  # noqa: PLC0415 — torch is plumbing for device memory
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("no HIP device visible to torch: the grammar masks run on the GPU only")
+    return torch
+
+
+class TokenBytes:
+    """A vocabulary's token byte strings on the device, as offsets + bytes."""
+
+    def __init__(self, vocab: Sequence[bytes], device: int = 0):
+        t = _torch()
+        lens = np.fromiter((len(b) for b in vocab), dtype=np.int64, count=len(vocab))
+        offsets = np.zeros(len(vocab) + 1, np.uint32)
+        if len(vocab):
+            offsets[1:] = np.cumsum(lens).astype(np.uint32)
+        flat = np.frombuffer(b"".join(bytes(b) for b in vocab), dtype=np.uint8)
+        dev = t.device("cuda", device)
+        self.vocab = len(vocab)
+        self.num_bytes = int(flat.shape[0])
+        self.offsets = t.from_numpy(offsets.view(np.int32).copy()).to(dev)
+        self.bytes = t.from_numpy(flat.copy() if flat.size else np.zeros(1, np.uint8)).to(dev)
+
+    def as_c(self) -> OxsTokenBytes:
+        return OxsTokenBytes(self.vocab, self.num_bytes, self.offsets.data_ptr(), self.bytes.data_ptr())
+
+
+class DfaSchemaGrammar:
+    """dfa.rs:4-12: num_states, a flat [num_states * 256] transition table, accepting states."""
+
+    def __init__(self, num_states: int, transitions: Sequence[int], accepting_states: Sequence[bool]):
+        self.num_states = int(num_states)
+        self.transitions = np.asarray(transitions, dtype=np.uint32).reshape(-1)
+        self.accepting_states = [bool(a) for a in accepting_states]
+        if self.transitions.shape[0] != self.num_states * 256:
+            raise ValueError("transitions must hold num_states * 256 entries")
+        self._dev = None
+
+    @classmethod
+    def new_simple_json_validator(cls) -> "DfaSchemaGrammar":
+        """dfa.rs:16-63: an 8-state JSON object validator."""
+        n = 8
+        t = np.full(n * 256, DFA_ERROR_STATE, np.uint32)
+        acc = [False] * n
+        t[ord("{")] = 1
+        t[256 + ord('"')] = 2
+        t[256 + ord("}")] = 7
+        t[2 * 256:3 * 256] = 2
+        t[2 * 256 + ord('"')] = 3
+        t[3 * 256 + ord(":")] = 4
+        for b in range(ord("0"), ord("9") + 1):
+            t[4 * 256 + b] = 5
+            t[5 * 256 + b] = 5
+        t[4 * 256 + ord('"')] = 6
+        t[5 * 256 + ord(",")] = 1
+        t[5 * 256 + ord("}")] = 7
+        t[6 * 256:7 * 256] = 6
+        t[6 * 256 + ord('"')] = 5
+        acc[7] = True
+        return cls(n, t, acc)
+
+    @classmethod
+    def new_json_with_fixed_prefix(cls, prefix: str) -> "DfaSchemaGrammar":
+        """dfa.rs:66-106: the prefix as a chain of states, then a number or string value and '}'."""
+        pb = prefix.encode()
+        plen = len(pb)
+        n = plen + 4
+        t = np.full(n * 256, DFA_ERROR_STATE, np.uint32)
+        acc = [False] * n
+        for i, b in enumerate(pb):
+            t[i * 256 + b] = i + 1
+        val, end, strv, term = plen, plen + 1, plen + 2, plen + 3
+        for b in range(ord("0"), ord("9") + 1):
+            t[val * 256 + b] = end
+            t[end * 256 + b] = end
+        t[val * 256 + ord('"')] = strv
+        t[end * 256 + ord("}")] = term
+        t[strv * 256:(strv + 1) * 256] = strv
+        t[strv * 256 + ord('"')] = end
+        acc[term] = True
+        return cls(n, t, acc)
+
+    def transition(self, current_state: int, byte: int) -> int:
+        """dfa.rs:110-126."""
+        if current_state >= self.num_states:
+            raise SchemaMismatch(current_state, byte)
+        nxt = int(self.transitions[current_state * 256 + byte])
+        if nxt == DFA_ERROR_STATE:
+            raise SchemaMismatch(current_state, byte)
+        return nxt
+
+    def deterministic_transition(self, current_state: int) -> Optional[int]:
+        """dfa.rs:151-168: the only byte with a transition, if there is exactly one."""
+        if current_state >= self.num_states:
+            return None
+        row = self.transitions[current_state * 256:(current_state + 1) * 256]
+        live = np.nonzero(row != DFA_ERROR_STATE)[0]
+        return int(live[0]) if live.shape[0] == 1 else None
+
+    def find_jump_forward_bytes(self, current_state: int, max_lookahead: int) -> Tuple[List[int], int]:
+        """dfa.rs:170-190: follow unambiguous arcs up to max_lookahead bytes."""
+        out: List[int] = []
+        while len(out) < max_lookahead:
+            b = self.deterministic_transition(current_state)
+            if b is None:
+                break
+            out.append(b)
+            current_state = int(self.transitions[current_state * 256 + b])
+            if current_state >= self.num_states or current_state == DFA_ERROR_STATE:
+                break
+        return out, current_state
+
+    def _device_table(self, device: int):
+        if self._dev is None:
+            t = _torch()
+            self._dev = t.from_numpy(self.transitions.view(np.int32).copy()).to(t.device("cuda", device))
+        return self._dev
+
+    def token_masks(self, token_bytes: TokenBytes, states, device: int = 0, stream=None):
+        """Packed masks [len(states), ceil(vocab / 32)] (int32 tensor on the GPU; bit set = allowed)."""
+        t = _torch()
+        lib = load_library()
+        dev = t.device("cuda", device)
+        st = states if hasattr(states, "data_ptr") else t.tensor(np.asarray(states, np.uint32).view(np.int32), device=dev)
+        st = st.to(dev).contiguous()
+        B = int(st.shape[0])
+        words = (token_bytes.vocab + 31) // 32
+        mask = t.empty(B, max(words, 1), dtype=t.int32, device=dev)
+        table = self._device_table(device)
+        dfa = OxsDfa(self.num_states, table.data_ptr() if self.num_states else 0)
+        tb = token_bytes.as_c()
+        s = stream if stream is not None else t.cuda.current_stream(dev)
+        check(lib.oxs_dfa_mask(ctypes.byref(dfa), ctypes.byref(tb), ctypes.c_void_p(st.data_ptr()), B,
+                               ctypes.c_void_p(mask.data_ptr()), mask.stride(0), ctypes.c_void_p(s.cuda_stream)),
+              "oxs_dfa_mask")
+        return mask[:, :words]
+
+    def apply_dfa_mask(self, current_state: int, token_bytes, logits) -> None:
+        """dfa.rs:130-148: tokens whose bytes do not walk from current_state get -inf (in place)."""
+        t = _torch()
+        tb = token_bytes if isinstance(token_bytes, TokenBytes) else TokenBytes(list(token_bytes))
+        words = self.token_masks(tb, [current_state])[0].cpu().numpy().view(np.uint32)
+        bits = np.unpackbits(words.view(np.uint8), bitorder="little")[: tb.vocab].astype(bool)
+        n = min(tb.vocab, len(logits))
+        if hasattr(logits, "masked_fill_"):
+            allowed = t.from_numpy(bits[:n].copy()).to(logits.device)
+            logits[:n].masked_fill_(~allowed, float("-inf"))
+        else:
+            for i in range(n):
+                if not bits[i]:
+                    logits[i] = float("-inf")
