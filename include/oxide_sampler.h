@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define OXS_ABI_VERSION 1u
+#define OXS_ABI_VERSION 2u
 
 /* Return codes. EngineError (crates/oxide-core/src/error.rs:6) has one variant
  * on this path, ShapeMismatch (error.rs:52; sampler.rs:179-181). */
@@ -210,6 +210,47 @@ size_t oxs_sampler_workspace_bytes(const oxs_sampler* sampler);
  * required pointers, OXS_ERR_HIP if the launch fails.
  */
 int oxs_sample_batch(oxs_sampler* sampler, const oxs_batch* batch, void* stream);
+
+/*
+ * Decode-loop state beside the sampler state (ActiveSequence,
+ * crates/oxide-engine/src/continuous_batching.rs:453-470), device arrays
+ * unless noted; every pointer is optional.
+ */
+typedef struct oxs_decode_io {
+  uint32_t* current_token;    /* [B] set to the sampled token: the next step's input (:974) */
+  int32_t* current_position;  /* [B] += 1 (:975) */
+  uint32_t* generated_count;  /* [B] += 1 (:976) */
+  /* Host memory from oxs_host_alloc (megakernel_ops.cu:331-347's h_sampled_token):
+   * host_tokens[B] receives the tokens and *host_seq is incremented once every
+   * row's host token is visible, so the host can poll it instead of
+   * synchronising the stream. */
+  uint32_t* host_tokens;
+  uint32_t* host_seq;
+} oxs_decode_io;
+
+/*
+ * One decode step of the scheduler's decode stage for B sequences at once
+ * (continuous_batching.rs:957-977), replacing its per-sequence loop:
+ *   - a row whose config has temperature <= 1e-6 takes the first largest of
+ *     its raw logits (:961-970): no penalties, filters or history, and its
+ *     rng_state, mirostat_mu and candidates buffer (out_kept_*) are left as
+ *     they were; the allowed mask, if any, still applies;
+ *   - every other row is sample_token(logits, state, newline_token_id)
+ *     exactly as in oxs_sample_batch (:971-972); a failing row gives token 0
+ *     (unwrap_or(0), :973);
+ *   - then io's arrays are advanced (:974-976) and the tokens handed to the
+ *     host. Calls that overlap on one sampler race on its step counter.
+ * Same arguments and errors as oxs_sample_batch, plus `io`; asynchronous;
+ * allocates nothing and issues only kernels, so it can be captured in a HIP
+ * graph. newline_token_id is the config's (the loop passes 10, :972).
+ */
+int oxs_decode_step(oxs_sampler* sampler, const oxs_batch* batch, const oxs_decode_io* io, void* stream);
+
+/* Page-locked host memory that the GPU writes directly (mapped, coherent; the
+ * same address on host and device), zeroed. For oxs_decode_io's host fields.
+ * OXS_ERR_UNSUPPORTED when the device address would differ from the host's. */
+int oxs_host_alloc(size_t bytes, void** out);
+int oxs_host_free(void* ptr);
 
 /*
  * Grammar masks from a DFA (the producer of oxs_batch.allowed_mask).

@@ -369,9 +369,28 @@ int oxo_sample_token(const oxs_sampling_config* cfg, const uint32_t* bias_ids,
   return sample_row(*cfg, bias_ids, bias_values, ban_ids, logits, vocab, io);
 }
 
-int oxo_sample_batch(const oxs_batch* b, int n_threads) {
+// continuous_batching.rs:961-970: the first index whose logit is larger than
+// every earlier one, starting from -inf at index 0 (so NaN never wins and a row
+// of -inf and NaN gives 0).
+static uint32_t raw_argmax(const float* row, uint32_t vocab) {
+  uint32_t best = 0;
+  float max_val = -INFINITY;
+  for (uint32_t i = 0; i < vocab; ++i) {
+    if (row[i] > max_val) {
+      max_val = row[i];
+      best = i;
+    }
+  }
+  return best;
+}
+
+// Rows of a batch (oxo_sample_batch), or of a decode step when `dec` is set:
+// then a row with temperature <= 1e-6 is the loop's raw argmax and touches no
+// sampler state, and every row advances the loop's per-sequence fields
+// (continuous_batching.rs:957-977).
+static int batch_rows(const oxs_batch* b, const oxs_decode_io* dec, int n_threads) {
   if (b->vocab == 0) return OXO_SHAPE_MISMATCH;
-  auto work = [b](uint32_t lo, uint32_t hi) {
+  auto work = [b, dec](uint32_t lo, uint32_t hi) {
     std::vector<float> row(b->vocab);
     for (uint32_t r = lo; r < hi; ++r) {
       const oxs_sampling_config& c = b->configs[(b->flags & OXS_FLAG_SHARED_CONFIG) ? 0 : r];
@@ -386,6 +405,17 @@ int oxo_sample_batch(const oxs_batch* b, int n_threads) {
         const uint32_t* m = b->allowed_mask + (size_t)r * b->mask_ld;
         for (uint32_t i = 0; i < b->vocab; ++i)
           if (!((m[i >> 5] >> (i & 31)) & 1u)) row[i] = -INFINITY;
+      }
+      if (dec && c.temperature <= 1e-6f) {  // :961-970
+        const uint32_t tok = raw_argmax(row.data(), b->vocab);
+        bool any = false;
+        for (uint32_t i = 0; i < b->vocab && !any; ++i) any = row[i] > -INFINITY;
+        b->out_tokens[r] = tok;
+        if (b->out_status) b->out_status[r] = any ? OXO_OK : OXO_EMPTY;
+        if (dec->current_token) dec->current_token[r] = tok;
+        if (dec->current_position) dec->current_position[r] += 1;
+        if (dec->generated_count) dec->generated_count[r] += 1;
+        continue;
       }
       uint32_t zero_len = 0;
       uint32_t* hist = b->history ? b->history + (size_t)r * b->history_ld : nullptr;
@@ -406,6 +436,11 @@ int oxo_sample_batch(const oxs_batch* b, int n_threads) {
       if (b->logits_out) memcpy(b->logits_out + (size_t)r * b->logits_out_ld, row.data(), sizeof(float) * b->vocab);
       b->out_tokens[r] = tok;
       if (b->out_status) b->out_status[r] = st;
+      if (dec) {  // :973-976 (every status here carries its token; errors give 0)
+        if (dec->current_token) dec->current_token[r] = tok;
+        if (dec->current_position) dec->current_position[r] += 1;
+        if (dec->generated_count) dec->generated_count[r] += 1;
+      }
     }
   };
   if (n_threads <= 1 || b->batch <= 1) {
@@ -422,6 +457,14 @@ int oxo_sample_batch(const oxs_batch* b, int n_threads) {
   }
   return 0;
 }
+
+int oxo_sample_batch(const oxs_batch* b, int n_threads) { return batch_rows(b, nullptr, n_threads); }
+
+int oxo_decode_step(const oxs_batch* b, const oxs_decode_io* io, int n_threads) {
+  return batch_rows(b, io, n_threads);
+}
+
+uint32_t oxo_raw_argmax(const float* row, uint32_t vocab) { return raw_argmax(row, vocab); }
 
 float oxo_expf(float x) { return expf(x); }
 float oxo_logf(float x) { return logf(x); }

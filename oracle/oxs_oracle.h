@@ -65,6 +65,21 @@ int oxo_sample_token(const oxs_sampling_config* cfg, const uint32_t* bias_ids,
 int oxo_sample_batch(const oxs_batch* batch, int n_threads);
 
 /*
+ * The decode stage of ContinuousBatchingEngine::step
+ * (crates/oxide-engine/src/continuous_batching.rs:957-977) over the same
+ * descriptor: a row with temperature <= 1e-6 takes oxo_raw_argmax of its
+ * (masked) logits and leaves history, mu, rng and the kept arrays alone; other
+ * rows are sampled as by oxo_sample_batch. Then io's current_token,
+ * current_position and generated_count advance (host pointers; the host_*
+ * fields are ignored).
+ */
+int oxo_decode_step(const oxs_batch* batch, const oxs_decode_io* io, int n_threads);
+
+/* continuous_batching.rs:961-970: first index of the largest logit, NaN never
+ * larger, 0 for a row with no value above -inf. */
+uint32_t oxo_raw_argmax(const float* row, uint32_t vocab);
+
+/*
  * StructuredOutputEngine::compute_token_mask (oxide-server/src/grammar_engine.rs:42-65),
  * equivalently the -inf pattern of DfaSchemaGrammar::apply_dfa_mask
  * (oxide-core/src/dfa.rs:130-148), for `batch` rows in states[b], as the packed

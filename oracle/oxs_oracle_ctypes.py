@@ -50,6 +50,10 @@ def load() -> ctypes.CDLL:
         getattr(lib, f).argtypes = [ctypes.c_float]
     lib.oxo_powf.restype = ctypes.c_float
     lib.oxo_powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    lib.oxo_decode_step.restype = ctypes.c_int
+    lib.oxo_decode_step.argtypes = [vp, vp, ctypes.c_int]
+    lib.oxo_raw_argmax.restype = ctypes.c_uint32
+    lib.oxo_raw_argmax.argtypes = [vp, ctypes.c_uint32]
     lib.oxo_dfa_mask.restype = None
     lib.oxo_dfa_mask.argtypes = [vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32,
                                  vp, ctypes.c_int64]
@@ -63,21 +67,24 @@ def _ptr(a):
 
 def sample_batch_host(abi, *, logits, dtype, configs_bytes, bias_ids, bias_values, ban_ids, mask, history,
                       history_len, history_cap, record, uniforms, rng_state, mu, kept_ld, logits_out=None,
-                      shared_config=False, n_threads=1):
+                      shared_config=False, n_threads=1, decode=None, kept_fill=0):
     """Runs the oracle over host numpy arrays with the oxs_batch descriptor.
 
     `abi` is the product's ctypes module (for the OxsBatch layout). Mutable
     arrays (history, history_len, rng_state, mu) are updated in place.
     Returns dict(tokens, status, kept_count, kept_ids, kept_probs).
+    With `decode` (a dict of current_token, current_position, generated_count
+    arrays, updated in place) it runs oxo_decode_step instead. The kept arrays
+    start filled with `kept_fill`.
     """
     lib = load()
     B, V = logits.shape
     out = {
         "tokens": np.zeros(B, np.uint32),
         "status": np.zeros(B, np.int32),
-        "kept_count": np.zeros(B, np.uint32),
-        "kept_ids": np.zeros((B, max(kept_ld, 1)), np.uint32),
-        "kept_probs": np.zeros((B, max(kept_ld, 1)), np.float32),
+        "kept_count": np.full(B, kept_fill, np.uint32),
+        "kept_ids": np.full((B, max(kept_ld, 1)), kept_fill, np.uint32),
+        "kept_probs": np.full((B, max(kept_ld, 1)), kept_fill, np.uint32).view(np.float32),
     }
     b = abi.OxsBatch()
     b.batch, b.vocab = B, V
@@ -109,7 +116,14 @@ def sample_batch_host(abi, *, logits, dtype, configs_bytes, bias_ids, bias_value
     if logits_out is not None:
         b.logits_out = logits_out.ctypes.data
         b.logits_out_ld = logits_out.shape[1]
-    rc = lib.oxo_sample_batch(ctypes.byref(b), n_threads)
+    if decode is None:
+        rc = lib.oxo_sample_batch(ctypes.byref(b), n_threads)
+    else:
+        io = abi.OxsDecodeIo()
+        io.current_token = _ptr(decode.get("current_token"))
+        io.current_position = _ptr(decode.get("current_position"))
+        io.generated_count = _ptr(decode.get("generated_count"))
+        rc = lib.oxo_decode_step(ctypes.byref(b), ctypes.byref(io), n_threads)
     if rc != 0:
         raise ValueError(f"oracle returned {rc}")
     return out
@@ -172,3 +186,9 @@ def dfa_mask_host(transitions, num_states, offsets, byte_arr, states):
                      _ptr(byte_arr) if byte_arr.size else None, byte_arr.shape[0], vocab, _ptr(states),
                      states.shape[0], _ptr(mask), mask.shape[1])
     return mask[:, :words]
+
+
+def raw_argmax_host(row) -> int:
+    """oxo_raw_argmax on one f32 row (continuous_batching.rs:961-970)."""
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    return int(load().oxo_raw_argmax(_ptr(row), row.shape[0]))

@@ -59,6 +59,7 @@ constexpr uint32_t kBanFlag = 1u << 28;
 constexpr uint32_t kBiasFlag = 1u << 29;
 constexpr uint32_t kNlFlag = 1u << 30;
 constexpr uint32_t kDryFlag = 1u << 31;  // exact-path table: the id has a DRY value
+constexpr uint32_t kFlagDecode = 1u << 31;  // Params.flags: a decode step (oxs_decode_step)
 
 struct Params {
   const void* logits;
@@ -99,6 +100,13 @@ struct Params {
   const uint64_t* libm;  // [kLibmWords]: the libm tables (exp2, 1/c, ln c, log2 c) as bit patterns
   uint64_t* dry_list;    // [B][kDryMax]: DRY rows' (id << 32 | value bits), sorted by id
   uint32_t* dry_count;   // [B]
+  // decode step (kFlagDecode): the decode loop's per-row state and host outputs
+  uint32_t* dec_token;    // [B] next step's input token
+  int32_t* dec_pos;       // [B] position
+  uint32_t* dec_count;    // [B] generated count
+  uint32_t* host_tokens;  // [B] host memory
+  uint32_t* host_seq;     // host memory: completed steps
+  uint32_t* ticket;       // rows finished in this launch (0 between launches)
 };
 
 // ---------------------------------------------------------------- keys
@@ -247,7 +255,34 @@ struct RowIn {
   float uniform;
   float mu;
   uint64_t rng;
+  bool raw;  // a decode-step row that takes the argmax of its raw logits
 };
+
+// The decode loop's greedy rows (continuous_batching.rs:961-970): a row with
+// temperature <= 1e-6 takes the first largest raw logit, with no penalty,
+// filter or sampler-state change. That is sample_token with every stage
+// disabled and the greedy draw (sampler.rs:371-372): the first candidate of
+// the pool sorted by value, then lower index (NaN and -inf are not
+// candidates, and a row without candidates gives 0, as the loop's initial
+// index does). The caller's state (history, mu, rng, candidates) is left
+// untouched.
+__device__ __forceinline__ void raw_argmax_config(oxs_sampling_config& c) {
+  c.temperature = 0.0f;
+  c.top_k = 0;
+  c.top_p = 1.0f;
+  c.min_p = 0.0f;
+  c.tfs_z = 1.0f;
+  c.typical_p = 1.0f;
+  c.xtc_probability = 0.0f;
+  c.mirostat_mode = OXS_MIROSTAT_DISABLED;
+  c.dry_multiplier = 0.0f;
+  c.repeat_penalty = 1.0f;
+  c.frequency_penalty = 0.0f;
+  c.presence_penalty = 0.0f;
+  c.penalize_nl = 0;
+  c.bias_count = 0;
+  c.ban_count = 0;
+}
 
 // Absent optional inputs read a valid dummy address (the config array) and
 // get their defaults.
@@ -287,6 +322,8 @@ __device__ __forceinline__ RowIn load_row_in(const Params& p, uint32_t row) {
   in.uniform = p.uniforms ? __uint_as_float(u) : 0.0f;
   in.mu = p.mu ? __uint_as_float(mu) : 0.0f;
   in.rng = p.rng_state ? (((uint64_t)rng[1] << 32) | rng[0]) : 0ull;
+  in.raw = (p.flags & kFlagDecode) && in.cfg.temperature <= 1e-6f;  // continuous_batching.rs:961
+  if (in.raw) raw_argmax_config(in.cfg);
   return in;
 }
 
@@ -1074,11 +1111,39 @@ __device__ __forceinline__ Chain seq_chain(const float* a, uint32_t n, float ini
   return Chain{n, s, false};
 }
 
-__device__ __forceinline__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status) {
+// The decode loop's bookkeeping once a row's token is known, by the thread
+// that wrote it (continuous_batching.rs:974-976; the device-side advance and
+// host hand-off of megakernel_ops.cu:331-347): the next step's input token,
+// position and generated count, the token in host memory and, from the row
+// that finishes last, the host's step counter, released after every row's
+// host token.
+__device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, uint32_t token) {
+  if (!(p.flags & kFlagDecode)) return;
+  if (p.dec_token) p.dec_token[row] = token;
+  if (p.dec_pos) p.dec_pos[row] += 1;
+  if (p.dec_count) p.dec_count[row] += 1u;
+  if (p.host_tokens) p.host_tokens[row] = token;
+  if (p.host_seq) {
+    __threadfence_system();  // this row's host token before its ticket
+    const uint32_t done = __hip_atomic_fetch_add(p.ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == p.B - 1u) {  // the last row: every other row's host token is visible
+      __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __threadfence_system();
+      const uint32_t n = __hip_atomic_load(p.host_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(p.host_seq, n + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+}
+
+// A row that ends before the chain. A raw decode row leaves the caller's
+// candidates buffer as it was.
+__device__ __forceinline__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status,
+                                                 bool raw) {
   if (threadIdx.x == 0) {
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
-    if (p.out_kept_count) p.out_kept_count[row] = 0;
+    if (p.out_kept_count && !raw) p.out_kept_count[row] = 0;
+    decode_advance(p, row, token);
   }
 }
 
@@ -1100,6 +1165,7 @@ struct RowState {
   float mu;
   uint64_t rng;
   uint32_t history_len;
+  bool raw;  // a raw decode row: no history, no candidates buffer
 };
 
 // Stable in-place compaction of (ids, pr)[0..len) by one wavefront: a step
@@ -1345,7 +1411,7 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
   // Outputs: token, status, history, candidates_buffer.
   if (l == 0) {
     int32_t status = OXS_ROW_OK;
-    if (p.flags & OXS_FLAG_RECORD_HISTORY) {
+    if ((p.flags & OXS_FLAG_RECORD_HISTORY) && !rs.raw) {
       uint32_t hl = rs.history_len;
       for (uint32_t k = 0; k < n_record; ++k) {
         if (hl < p.history_cap) {
@@ -1359,9 +1425,10 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
     }
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
-    if (p.out_kept_count) p.out_kept_count[row] = len;
+    if (p.out_kept_count && !rs.raw) p.out_kept_count[row] = len;
+    decode_advance(p, row, token);
   }
-  const uint32_t nk = (uint32_t)min((int64_t)len, p.kept_ld);
+  const uint32_t nk = rs.raw ? 0u : (uint32_t)min((int64_t)len, p.kept_ld);
   for (uint32_t i = l; i < nk; i += 64) {
     if (p.out_kept_ids) p.out_kept_ids[(size_t)row * p.kept_ld + i] = ids[i];
     if (p.out_kept_probs) p.out_kept_probs[(size_t)row * p.kept_ld + i] = (pr[i] * k_in) * inv_total;
@@ -1564,17 +1631,18 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   rs.mu = rin.mu;
   rs.rng = rin.rng;
   rs.history_len = rin.history_len;
+  rs.raw = rin.raw;
   store_libm_tables(tabv, s_tab);
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
 
 
   const uint32_t M = max(c.top_k, 256u);
   if (M > (uint32_t)kMaxM || (r.dry && min(r.hlen, r.dry_range) > (uint32_t)kDryMax)) {
-    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED);  // sizes this build does not run on the device
+    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED, rin.raw);  // sizes this build does not run on the device
     return;
   }
   if (c.mirostat_mode != OXS_MIROSTAT_DISABLED && !p.mu) {
-    write_row_result(p, row, 0u, OXS_ROW_MISSING_STATE);
+    write_row_result(p, row, 0u, OXS_ROW_MISSING_STATE, rin.raw);
     return;
   }
   // DRY rows: their values, then the exact path (the stream kernel's
@@ -1677,7 +1745,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
 
   if (path == 0) {
     if (meff == 0) {  // every logit -inf or NaN (:267-270)
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY);
+      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rin.raw);
       return;
     }
     const uint32_t span_k = s_bstart[last] + s_bcount[last];  // keys in buckets 0 .. last
@@ -1709,7 +1777,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     } else {
       meff = min(M, N);
       if (meff == 0) {
-        write_row_result(p, row, 0u, OXS_ROW_EMPTY);
+        write_row_result(p, row, 0u, OXS_ROW_EMPTY, rin.raw);
         return;
       }
       keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
@@ -1718,7 +1786,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   if (path == 2) {
     meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)s_keys, s_bcount, s_top, ts);
     if (meff == 0) {
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY);
+      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rin.raw);
       return;
     }
     bitonic_sort<false>(s_top, meff);
@@ -1828,6 +1896,7 @@ struct oxs_sampler {
   uint64_t* libm;
   uint64_t* dry_list;
   uint32_t* dry_count;
+  uint32_t* ticket;  // decode steps: rows finished in the running launch
   size_t bytes;
 };
 
@@ -1907,9 +1976,10 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
                   hipMalloc((void**)&s->wave_count, b_count) == hipSuccess &&
                   hipMalloc((void**)&s->libm, oxs::kLibmWords * sizeof(uint64_t)) == hipSuccess &&
                   hipMalloc((void**)&s->dry_list, B * oxs::kDryMax * sizeof(uint64_t)) == hipSuccess &&
-                  hipMalloc((void**)&s->dry_count, B * sizeof(uint32_t)) == hipSuccess;
+                  hipMalloc((void**)&s->dry_count, B * sizeof(uint32_t)) == hipSuccess &&
+                  hipMalloc((void**)&s->ticket, 256) == hipSuccess && hipMemset(s->ticket, 0, 256) == hipSuccess;
   s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t) +
-             B * (oxs::kDryMax * sizeof(uint64_t) + sizeof(uint32_t));
+             B * (oxs::kDryMax * sizeof(uint64_t) + sizeof(uint32_t)) + 256;
   if (ok) {  // the libm tables, as bit patterns, in the workspace
     uint64_t host[oxs::kLibmWords];
     ok = hipMemcpyFromSymbol(host, HIP_SYMBOL(oxs_libm::kExp2Tab), 32 * sizeof(uint64_t)) == hipSuccess &&
@@ -1934,13 +2004,17 @@ int oxs_sampler_destroy(oxs_sampler* s) {
   if (s->libm) (void)hipFree(s->libm);
   if (s->dry_list) (void)hipFree(s->dry_list);
   if (s->dry_count) (void)hipFree(s->dry_count);
+  if (s->ticket) (void)hipFree(s->ticket);
   free(s);
   return OXS_OK;
 }
 
 size_t oxs_sampler_workspace_bytes(const oxs_sampler* s) { return s ? s->bytes : 0; }
 
-int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
+}  // extern "C"
+
+// One sampling launch pair; `io` (a decode step) may be NULL.
+static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* io, void* stream) {
   using namespace oxs;
   if (!s || !b) return OXS_ERR_INVALID_ARGUMENT;
   if (b->vocab == 0) return OXS_ERR_SHAPE_MISMATCH;  // sampler.rs:179-181
@@ -2008,6 +2082,15 @@ int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
   p.libm = s->libm;
   p.dry_list = s->dry_list;
   p.dry_count = s->dry_count;
+  if (io) {
+    p.flags |= kFlagDecode;
+    p.dec_token = io->current_token;
+    p.dec_pos = io->current_position;
+    p.dec_count = io->generated_count;
+    p.host_tokens = io->host_tokens;
+    p.host_seq = io->host_seq;
+    p.ticket = s->ticket;
+  }
   // Group rows by XCD when the batch divides evenly over the 8 XCDs.
   p.rpx = (b->batch % 8 == 0) ? b->batch / 8 : 0;
   const uint32_t epl = b->logits_dtype == OXS_DTYPE_F32 ? 4 : 8;
@@ -2021,6 +2104,39 @@ int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
                            ? launch_all<OXS_DTYPE_F32>(g.slots, vec, mask, p, grid_a, grid_b, st)
                            : launch_all<OXS_DTYPE_BF16>(g.slots, vec, mask, p, grid_a, grid_b, st);
   return e == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+}
+
+extern "C" {
+
+int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
+  if (b && (b->flags & oxs::kFlagDecode)) return OXS_ERR_INVALID_ARGUMENT;  // not a public flag
+  return sample_impl(s, b, nullptr, stream);
+}
+
+int oxs_decode_step(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* io, void* stream) {
+  if (!io || (b && (b->flags & oxs::kFlagDecode))) return OXS_ERR_INVALID_ARGUMENT;
+  return sample_impl(s, b, io, stream);
+}
+
+int oxs_host_alloc(size_t bytes, void** out) {
+  if (!out || bytes == 0) return OXS_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  // mapped and coherent: the GPU's stores reach the host without a copy
+  void* h = nullptr;
+  if (hipHostMalloc(&h, bytes, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) return OXS_ERR_HIP;
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || d != h) {  // one address on both sides
+    (void)hipHostFree(h);
+    return OXS_ERR_UNSUPPORTED;
+  }
+  memset(h, 0, bytes);
+  *out = h;
+  return OXS_OK;
+}
+
+int oxs_host_free(void* ptr) {
+  if (!ptr) return OXS_OK;
+  return hipHostFree(ptr) == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }
 
 }  // extern "C"

@@ -1,6 +1,6 @@
 """Python view of the MI355X batched token sampler (liboxide_sampler.so).
 
-Three layers, all thin over the C ABI in include/oxide_sampler.h:
+Four layers, all thin over the C ABI in include/oxide_sampler.h:
 
 - `BatchSampler`: the batched device call, `oxs_sample_batch`, on torch
   tensors that already live on the GPU (the decode-loop form).
@@ -9,6 +9,9 @@ Three layers, all thin over the C ABI in include/oxide_sampler.h:
   same names and argument meaning, each call running one row on the GPU.
 - `DfaSchemaGrammar`: the reference's grammar DFA (crates/oxide-core/src/dfa.rs),
   whose token masks run on the GPU (`oxs_dfa_mask`) and feed the sampler.
+- `DecodeLoop`: the scheduler's decode stage
+  (crates/oxide-engine/src/continuous_batching.rs:940-1040) with every
+  sequence's sampler state on the device, one `oxs_decode_step` per step.
 
 There is no CPU path: without the built library every call raises
 `LibraryMissing`.
@@ -23,6 +26,7 @@ from .engine import (
     configs_to_array,
 )
 from .grammar import DfaSchemaGrammar, SchemaMismatch, TokenBytes
+from .decode import DecodeLoop, TokenEvent
 from ._abi import (
     LibraryMissing,
     OxsError,
@@ -40,6 +44,8 @@ __all__ = [
     "DfaSchemaGrammar",
     "SchemaMismatch",
     "TokenBytes",
+    "DecodeLoop",
+    "TokenEvent",
     "LibraryMissing",
     "OxsError",
     "load_library",

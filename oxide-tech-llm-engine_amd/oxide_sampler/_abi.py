@@ -12,7 +12,7 @@ from pathlib import Path
 PKG_ROOT = Path(__file__).resolve().parent.parent  # oxide-tech-llm-engine_amd/
 LIB_PATH = PKG_ROOT / "lib" / "liboxide_sampler.so"
 
-OXS_ABI_VERSION = 1
+OXS_ABI_VERSION = 2
 
 OXS_OK = 0
 OXS_ERR_INVALID_ARGUMENT = -1
@@ -49,6 +49,9 @@ EXPORTED_SYMBOLS = (
     "oxs_sampler_destroy",
     "oxs_sampler_workspace_bytes",
     "oxs_sample_batch",
+    "oxs_decode_step",
+    "oxs_host_alloc",
+    "oxs_host_free",
     "oxs_dfa_mask",
 )
 
@@ -142,6 +145,16 @@ class OxsTokenBytes(ctypes.Structure):
     ]
 
 
+class OxsDecodeIo(ctypes.Structure):
+    _fields_ = [
+        ("current_token", ctypes.c_void_p),
+        ("current_position", ctypes.c_void_p),
+        ("generated_count", ctypes.c_void_p),
+        ("host_tokens", ctypes.c_void_p),
+        ("host_seq", ctypes.c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -178,6 +191,13 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_sampler_workspace_bytes.argtypes = [ctypes.c_void_p]
     lib.oxs_sample_batch.restype = ctypes.c_int
     lib.oxs_sample_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.c_void_p]
+    lib.oxs_decode_step.restype = ctypes.c_int
+    lib.oxs_decode_step.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.POINTER(OxsDecodeIo),
+                                    ctypes.c_void_p]
+    lib.oxs_host_alloc.restype = ctypes.c_int
+    lib.oxs_host_alloc.argtypes = [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]
+    lib.oxs_host_free.restype = ctypes.c_int
+    lib.oxs_host_free.argtypes = [ctypes.c_void_p]
     lib.oxs_dfa_mask.restype = ctypes.c_int
     lib.oxs_dfa_mask.argtypes = [ctypes.POINTER(OxsDfa), ctypes.POINTER(OxsTokenBytes), ctypes.c_void_p,
                                  ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]

@@ -17,7 +17,7 @@ from typing import Dict, Iterable, List, Optional, Sequence, Set, Tuple
 import numpy as np
 
 from . import _abi
-from ._abi import OxsBatch, OxsLimits, OxsSamplingConfig, check, load_library
+from ._abi import OxsBatch, OxsDecodeIo, OxsLimits, OxsSamplingConfig, check, load_library
 
 _DEFAULT_RNG = 0x853C49E6748FEA9B  # SamplerState::default() (sampler.rs:98)
 _MASK64 = (1 << 64) - 1
@@ -192,21 +192,29 @@ class BatchSampler:
     def workspace_bytes(self) -> int:
         return int(self.lib.oxs_sampler_workspace_bytes(self.handle))
 
-    def launch(self, batch: OxsBatch, stream=None) -> None:
-        """Raw launch of a prepared descriptor on `stream` (torch stream or None)."""
+    def launch(self, batch: OxsBatch, stream=None, decode: Optional[OxsDecodeIo] = None) -> None:
+        """Raw launch of a prepared descriptor on `stream` (torch stream or None);
+        with `decode`, a decode step (oxs_decode_step)."""
         s = stream if stream is not None else self.torch.cuda.current_stream(self.device)
-        check(self.lib.oxs_sample_batch(self.handle, ctypes.byref(batch), ctypes.c_void_p(s.cuda_stream)),
-              "oxs_sample_batch")
+        if decode is None:
+            check(self.lib.oxs_sample_batch(self.handle, ctypes.byref(batch), ctypes.c_void_p(s.cuda_stream)),
+                  "oxs_sample_batch")
+        else:
+            check(self.lib.oxs_decode_step(self.handle, ctypes.byref(batch), ctypes.byref(decode),
+                                           ctypes.c_void_p(s.cuda_stream)), "oxs_decode_step")
 
     def sample(self, logits, configs, *, bias_ids=None, bias_values=None, ban_ids=None, shared_config=False,
                mask=None, history=None, history_len=None, history_cap: Optional[int] = None,
                record: bool = False, uniforms=None, rng_state=None, mirostat_mu=None,
-               kept_ld: int = 0, logits_out=None, stream=None):
+               kept_ld: int = 0, logits_out=None, stream=None, decode: Optional[OxsDecodeIo] = None,
+               out: Optional[dict] = None):
         """Samples every row of `logits` ([B, V] f32/bf16 CUDA tensor).
 
         `configs` is a uint8 CUDA tensor holding B (or 1 with shared_config)
         packed `oxs_sampling_config` records. Returns a dict of output tensors
-        (tokens, status, kept_count and, with kept_ld > 0, kept_ids/kept_probs).
+        (tokens, status, kept_count and, with kept_ld > 0, kept_ids/kept_probs),
+        the ones of `out` when given. With `decode` (an OxsDecodeIo) the call
+        is a decode step (oxs_decode_step).
         """
         t = self.torch
         dev = logits.device
@@ -217,11 +225,10 @@ class BatchSampler:
             dtype = _abi.OXS_DTYPE_BF16
         else:
             raise TypeError(f"logits dtype {logits.dtype} is not float32 or bfloat16")
-        out = {
-            "tokens": t.empty(B, dtype=t.int32, device=dev),
-            "status": t.empty(B, dtype=t.int32, device=dev),
-            "kept_count": t.empty(B, dtype=t.int32, device=dev),
-        }
+        out = dict(out) if out is not None else {}
+        for k in ("tokens", "status", "kept_count"):
+            if k not in out:
+                out[k] = t.empty(B, dtype=t.int32, device=dev)
         b = OxsBatch()
         b.batch, b.vocab, b.logits_dtype = B, V, dtype
         b.flags = (_abi.OXS_FLAG_RECORD_HISTORY if record else 0) | (_abi.OXS_FLAG_SHARED_CONFIG if shared_config else 0)
@@ -251,15 +258,17 @@ class BatchSampler:
         b.out_status = out["status"].data_ptr()
         b.out_kept_count = out["kept_count"].data_ptr()
         if kept_ld > 0:
-            out["kept_ids"] = t.empty(B, kept_ld, dtype=t.int32, device=dev)
-            out["kept_probs"] = t.empty(B, kept_ld, dtype=t.float32, device=dev)
+            if "kept_ids" not in out:
+                out["kept_ids"] = t.empty(B, kept_ld, dtype=t.int32, device=dev)
+            if "kept_probs" not in out:
+                out["kept_probs"] = t.empty(B, kept_ld, dtype=t.float32, device=dev)
             b.out_kept_ids = out["kept_ids"].data_ptr()
             b.out_kept_probs = out["kept_probs"].data_ptr()
             b.kept_ld = kept_ld
         if logits_out is not None:
             b.logits_out = logits_out.data_ptr()
             b.logits_out_ld = int(logits_out.stride(0))
-        self.launch(b, stream)
+        self.launch(b, stream, decode)
         return out
 
 

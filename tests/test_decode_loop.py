@@ -1,0 +1,332 @@
+"""The decode stage: oxs_decode_step and DecodeLoop against the oracle.
+
+Reference: crates/oxide-engine/src/continuous_batching.rs:940-1040 (the
+scheduler's decode stage) and megakernel_ops.cu:331-347 (the device-side
+advance and host hand-off).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oxs_oracle_ctypes as oracle
+from oxide_sampler import _abi
+from oxide_sampler.decode import STOP_TOKENS, Sequence, next_event
+from oxide_sampler.engine import MirostatMode, SamplerState, SamplingConfig, configs_to_array
+from oxide_sampler.grammar import DfaSchemaGrammar
+
+SENT = 0xA5A5A5A5  # fills the kept arrays: a raw-argmax row must leave them as they were
+
+
+# ----------------------------------------------------------------------------- the oracle's raw argmax
+
+def test_raw_argmax_special_cases():
+    # continuous_batching.rs:961-970: strict '>' from -inf at index 0
+    inf, nan = np.inf, np.nan
+    cases = [
+        ([1.0, 3.0, 3.0, 2.0], 1),       # first of equal maxima
+        ([-inf, -inf], 0),               # nothing above -inf: the initial index
+        ([nan, nan, nan], 0),            # NaN is never larger
+        ([nan, 1.0, nan, 0.5], 1),
+        ([-inf, nan, -5.0], 2),
+        ([2.0, inf, 7.0, inf], 1),       # first +inf
+        ([-0.0, 0.0], 0),                # 0.0 > -0.0 is false
+        ([-3e38, -inf, -2e38], 2),
+    ]
+    for row, want in cases:
+        assert oracle.raw_argmax_host(np.array(row, np.float32)) == want, row
+
+
+def test_raw_argmax_matches_numpy():
+    rng = np.random.default_rng(7)
+    for n in (1, 2, 17, 1000, 32000):
+        x = rng.standard_normal(n).astype(np.float32)
+        x[rng.random(n) < 0.1] = np.nan
+        x[rng.random(n) < 0.1] = -np.inf
+        if n > 3:
+            x[n // 3] = x[2 * n // 3] = np.float32(9.0)  # a tie for the maximum
+        y = np.where(np.isnan(x), -np.inf, x)
+        want = int(np.argmax(y))  # numpy's argmax returns the first maximum
+        assert oracle.raw_argmax_host(x) == want
+
+
+# ----------------------------------------------------------------------------- a decode-step workload
+
+def decode_configs():
+    C = SamplingConfig
+    rows = [
+        C(temperature=0.8, top_p=0.95),                           # the loop's own config (:446-450)
+        C(temperature=0.0, top_p=0.9),                            # raw argmax (:961)
+        C(temperature=1e-6, repeat_penalty=2.0),                  # raw: penalties do not apply
+        C(temperature=2e-6, top_k=0, min_p=0.0),                  # sampled, scaled by 1/T
+        C(temperature=float("nan")),                              # NaN <= 1e-6 is false: sampled, no scaling
+        C(temperature=1.0, top_k=0, mirostat_mode=MirostatMode.V2),
+        C(temperature=0.7, frequency_penalty=0.3, presence_penalty=0.2, repeat_penalty=1.05, repeat_last_n=0,
+          top_k=50, top_p=0.9),
+        C(temperature=0.9, dry_multiplier=0.8, dry_allowed_length=2, top_k=0, min_p=0.0, top_p=0.97),
+        C(temperature=1.2, typical_p=0.9, tfs_z=0.95, top_k=0, min_p=0.0),
+        C(temperature=0.5, xtc_probability=0.5, xtc_threshold=0.05, min_p=0.0),
+        C(temperature=1.0, mirostat_mode=MirostatMode.V1),
+        C(temperature=-1.0, penalize_nl=True),                    # raw
+    ]
+    return rows + rows
+
+
+def decode_state(B, cap, seed):
+    rng = np.random.default_rng(seed)
+    history = np.zeros((B, cap), np.uint32)
+    hlen = rng.integers(0, 24, size=B).astype(np.uint32)
+    motif = rng.integers(0, 50, size=6)
+    for b in range(B):
+        h = np.concatenate([motif, rng.integers(0, 400, size=40), motif])[: hlen[b]]
+        history[b, : hlen[b]] = h
+    hlen[5] = cap - 1  # the Mirostat row records twice per step: its history fills
+    mu = np.full(B, 10.0, np.float32)  # SamplerState::new(5.0)
+    rng_state = np.array([0x853C49E6748FEA9B + 977 * b for b in range(B)], np.uint64)
+    dec = {"current_token": rng.integers(0, 1000, size=B).astype(np.uint32),
+           "current_position": rng.integers(0, 5000, size=B).astype(np.int32),
+           "generated_count": rng.integers(0, 50, size=B).astype(np.uint32)}
+    return history, hlen, mu, rng_state, dec
+
+
+def decode_logits(B, V, step, history, hlen):
+    rng = np.random.default_rng(1000 + step)
+    x = (rng.standard_normal((B, V), dtype=np.float32) * np.float32(2.0))
+    for b in range(B):  # recent history ids strong, so the penalties matter
+        n = int(hlen[b])
+        if n:
+            ids = history[b, max(0, n - 8):n]
+            x[b, ids] += np.float32(4.0)
+    x[1, 10:14] = np.float32(50.0)         # a tie for the raw argmax
+    if step == 2:
+        x[2, :] = -np.inf                   # raw row with no candidate: token 0
+        x[0, :] = -np.inf                   # sampled row with no candidate: EMPTY, nothing recorded
+    if step == 3:
+        x[1, ::3] = np.nan
+        x[6, ::5] = np.nan
+    return x
+
+
+def oracle_decode(cfg_bytes, logits, history, hlen, mu, rng_state, dec, cap):
+    return oracle.sample_batch_host(
+        _abi, logits=logits, dtype="f32", configs_bytes=cfg_bytes, bias_ids=None, bias_values=None, ban_ids=None,
+        mask=None, history=history, history_len=hlen, history_cap=cap, record=True, uniforms=None,
+        rng_state=rng_state, mu=mu, kept_ld=256, decode=dec, kept_fill=SENT)
+
+
+def test_oracle_decode_step_is_sample_batch_plus_raw_rows():
+    B, V, cap = 24, 3001, 64
+    cfgs = decode_configs()
+    cfg_bytes = configs_to_array(cfgs, 10)[0]
+    history, hlen, mu, rng_state, dec = decode_state(B, cap, 3)
+    logits = decode_logits(B, V, 1, history, hlen)
+    h2, l2, m2, r2 = history.copy(), hlen.copy(), mu.copy(), rng_state.copy()
+    d0 = {k: v.copy() for k, v in dec.items()}
+    got = oracle_decode(cfg_bytes, logits, history, hlen, mu, rng_state, dec, cap)
+    ref = oracle.sample_batch_host(
+        _abi, logits=logits, dtype="f32", configs_bytes=cfg_bytes, bias_ids=None, bias_values=None, ban_ids=None,
+        mask=None, history=h2, history_len=l2, history_cap=cap, record=True, uniforms=None, rng_state=r2, mu=m2,
+        kept_ld=256, kept_fill=SENT)
+    raw = np.array([c.temperature <= 1e-6 for c in cfgs])
+    for b in range(B):
+        if raw[b]:
+            assert got["tokens"][b] == oracle.raw_argmax_host(logits[b])
+            assert got["kept_count"][b] == SENT and (got["kept_ids"][b] == SENT).all()
+        else:
+            assert got["tokens"][b] == ref["tokens"][b] and got["status"][b] == ref["status"][b]
+            np.testing.assert_array_equal(got["kept_ids"][b], ref["kept_ids"][b])
+    # raw rows: the sampler state is untouched; sampled rows: as sample_batch left it
+    assert (history[raw] == decode_state(B, cap, 3)[0][raw]).all()
+    np.testing.assert_array_equal(hlen[~raw], l2[~raw])
+    np.testing.assert_array_equal(rng_state[~raw], r2[~raw])
+    np.testing.assert_array_equal(rng_state[raw], decode_state(B, cap, 3)[3][raw])
+    np.testing.assert_array_equal(dec["current_token"], got["tokens"])
+    np.testing.assert_array_equal(dec["current_position"], d0["current_position"] + 1)
+    np.testing.assert_array_equal(dec["generated_count"], d0["generated_count"] + 1)
+
+
+# ----------------------------------------------------------------------------- the host bookkeeping
+
+def test_next_event_stop_length_and_dfa():
+    # :986-1030 — stop tokens without a tokenizer, max_tokens, DFA accepting states
+    ev = next_event(Sequence(3, 0.8, 1), 128_009)
+    assert ev.is_terminal and ev.finish_reason == "stop"
+    ev = next_event(Sequence(3, 0.8, 3), 500)
+    assert ev.is_terminal and ev.finish_reason == "length"
+    ev = next_event(Sequence(3, 0.8, 2), 500)
+    assert not ev.is_terminal and ev.finish_reason is None
+    assert all(t in STOP_TOKENS for t in (0, 2, 128_001, 128_008, 128_009, 151_643, 151_645))
+    # a DFA walk over the token's low byte; bytes with no transition keep the state
+    dfa = DfaSchemaGrammar.new_simple_json_validator()
+    seq = Sequence(100, 0.8, 1, dfa, 0)
+    for tok in (ord("{"), ord("x"), ord('"'), ord("k"), ord('"'), ord(":"), ord("7")):
+        assert not next_event(seq, tok + 256).is_terminal  # + 256: only the low byte counts
+    assert seq.dfa_state == 5
+    ev = next_event(seq, ord("}"))
+    assert ev.is_terminal and ev.finish_reason == "stop" and seq.dfa_state == 7
+    # with a tokenizer's bytes
+    seq = Sequence(100, 0.8, 1, dfa, 0)
+    next_event(seq, 9999, token_bytes=lambda t: b'{"ab"')
+    assert seq.dfa_state == 3
+
+
+# ----------------------------------------------------------------------------- the GPU
+
+def _to_dev(torch, a, dtype=None):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    elif a.dtype == np.uint64:
+        a = a.view(np.int64)
+    return torch.from_numpy(a.copy()).to("cuda")
+
+
+def _u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.gpu
+def test_gpu_decode_steps_match_oracle(torch_gpu):
+    from oxide_sampler import BatchSampler
+    from oxide_sampler._abi import OxsDecodeIo
+    t = torch_gpu
+    B, V, cap, steps = 24, 50001, 64, 5
+    cfgs = decode_configs()
+    cfg_bytes = configs_to_array(cfgs, 10)[0]
+    history, hlen, mu, rng_state, dec = decode_state(B, cap, 11)
+    d_cfg = _to_dev(t, cfg_bytes)
+    d_hist, d_hlen, d_mu, d_rng = (_to_dev(t, a) for a in (history, hlen, mu, rng_state))
+    d_dec = {k: _to_dev(t, v) for k, v in dec.items()}
+    lib = _abi.load_library()
+    host = ctypes.c_void_p()
+    _abi.check(lib.oxs_host_alloc(64 + 4 * B, ctypes.byref(host)), "oxs_host_alloc")
+    try:
+        io = OxsDecodeIo(d_dec["current_token"].data_ptr(), d_dec["current_position"].data_ptr(),
+                         d_dec["generated_count"].data_ptr(), host.value + 64, host.value)
+        s = BatchSampler(B, V, 256)
+        out = {"tokens": t.zeros(B, dtype=t.int32, device="cuda"),
+               "status": t.zeros(B, dtype=t.int32, device="cuda"),
+               "kept_count": t.zeros(B, dtype=t.int32, device="cuda"),
+               "kept_ids": t.zeros(B, 256, dtype=t.int32, device="cuda"),
+               "kept_probs": t.zeros(B, 256, dtype=t.float32, device="cuda")}
+        sent = int(np.uint32(SENT).view(np.int32))
+        for step in range(steps):
+            print(f"\n[case] decode step {step} B={B} V={V}", flush=True)
+            logits = decode_logits(B, V, step, history, hlen)
+            for k in ("kept_count", "kept_ids"):
+                out[k].fill_(sent)
+            out["kept_probs"].view(t.int32).fill_(sent)
+            s.sample(_to_dev(t, logits), d_cfg, history=d_hist, history_len=d_hlen, history_cap=cap, record=True,
+                     rng_state=d_rng, mirostat_mu=d_mu, kept_ld=256, decode=io, out=out)
+            t.cuda.synchronize()
+            ref = oracle_decode(cfg_bytes, logits, history, hlen, mu, rng_state, dec, cap)
+            np.testing.assert_array_equal(_u32(out["tokens"]), ref["tokens"])
+            np.testing.assert_array_equal(out["status"].cpu().numpy(), ref["status"])
+            np.testing.assert_array_equal(_u32(out["kept_count"]), ref["kept_count"])
+            kc = ref["kept_count"]
+            kid, kpr = _u32(out["kept_ids"]), out["kept_probs"].cpu().numpy().view(np.uint32)
+            for b in range(B):
+                n = 256 if kc[b] == SENT else int(kc[b])
+                np.testing.assert_array_equal(kid[b, :n], ref["kept_ids"][b, :n])
+                np.testing.assert_array_equal(kpr[b, :n], ref["kept_probs"][b, :n].view(np.uint32))
+            np.testing.assert_array_equal(_u32(d_hlen), hlen)
+            np.testing.assert_array_equal(_u32(d_hist), history)
+            np.testing.assert_array_equal(d_mu.cpu().numpy().view(np.uint32), mu.view(np.uint32))
+            np.testing.assert_array_equal(d_rng.cpu().numpy().view(np.uint64), rng_state)
+            for k in dec:
+                np.testing.assert_array_equal(d_dec[k].cpu().numpy().view(dec[k].dtype), dec[k])
+            host_tokens = np.ctypeslib.as_array((ctypes.c_uint32 * B).from_address(host.value + 64)).copy()
+            np.testing.assert_array_equal(host_tokens, ref["tokens"])
+            assert ctypes.c_uint32.from_address(host.value).value == step + 1
+        raw = np.array([c.temperature <= 1e-6 for c in cfgs])
+        assert (ref["status"][~raw] == _abi.OXS_ROW_HISTORY_FULL).any()  # the filled history was reached
+        s.close()
+    finally:
+        t.cuda.synchronize()
+        lib.oxs_host_free(host)
+
+
+def _loop_with(torch, cfgs, V, cap=128):
+    from oxide_sampler import DecodeLoop
+    loop = DecodeLoop(len(cfgs), V, history_cap=cap)
+    for slot, c in enumerate(cfgs):
+        loop.add_sequence(slot, temperature=c.temperature, top_p=c.top_p, current_token=slot, current_position=7,
+                          max_tokens=1000, config=c)
+    return loop
+
+
+@pytest.mark.gpu
+def test_gpu_decode_loop_host_poll_and_graph_replays(torch_gpu):
+    t = torch_gpu
+    cfgs = decode_configs()[:12]
+    B, V = len(cfgs), 32000
+    eager = _loop_with(t, cfgs, V)
+    graphed = _loop_with(t, cfgs, V)
+    static = t.zeros(B, V, dtype=t.float32, device="cuda")
+    graphed.capture(static)
+    hist = np.zeros((B, 1), np.uint32)
+    for step in range(6):
+        print(f"\n[case] decode loop step {step}: eager, then graph replay", flush=True)
+        x = decode_logits(B, V, step + 10, hist, np.zeros(B, np.uint32))
+        n = eager.launch(_to_dev(t, x))
+        tok_e = eager.wait(n)  # polled from host memory, no stream sync
+        static.copy_(_to_dev(t, x))
+        m = graphed.replay()
+        tok_g = graphed.wait(m)
+        assert eager.completed() == step + 1 and graphed.completed() == step + 1
+        np.testing.assert_array_equal(tok_g, tok_e)
+        t.cuda.synchronize()
+        np.testing.assert_array_equal(_u32(eager.out["tokens"]), tok_e)
+        for name in ("history", "history_len", "mirostat_mu", "rng_state", "current_token", "current_position",
+                     "generated_count"):
+            a, b = getattr(eager, name), getattr(graphed, name)
+            assert t.equal(a, b), (step, name)
+    # raw slots (temperature <= 1e-6) kept their state; the others recorded
+    for slot, c in enumerate(cfgs):
+        st = eager.state(slot)
+        if c.temperature <= 1e-6:
+            assert st.generated_tokens == [] and st.rng_state == SamplerState.new(5.0).rng_state
+        assert int(eager.current_position[slot]) == 7 + 6 and int(eager.generated_count[slot]) == 6
+    eager.close()
+    graphed.close()
+
+
+@pytest.mark.gpu
+def test_gpu_decode_loop_events_match_reference_loop(torch_gpu):
+    # DecodeLoop.step against the reference loop run on the oracle, sequence by sequence
+    t = torch_gpu
+    V, B, steps = 4096, 8, 12
+    from oxide_sampler import DecodeLoop
+    loop = DecodeLoop(B, V, history_cap=64)
+    dfa = DfaSchemaGrammar.new_simple_json_validator()
+    specs = [(0.8, 0.95, 5, None), (0.0, 1.0, 100, None), (1.0, 0.9, 100, dfa), (0.5, 0.5, 3, None),
+             (0.9, 0.95, 100, dfa), (1e-7, 0.95, 4, dfa)]
+    ref_state = {}
+    for slot, (temp, top_p, max_tok, g) in enumerate(specs):
+        loop.add_sequence(slot, temperature=temp, top_p=top_p, current_token=1, current_position=0,
+                          max_tokens=max_tok, dfa=g)
+        ref_state[slot] = (SamplerState.new(5.0), Sequence(max_tok, temp, 0, g, 0),
+                           SamplingConfig(temperature=temp, top_p=top_p))
+    rng = np.random.default_rng(5)
+    for step in range(steps):
+        x = (rng.standard_normal((B, V), dtype=np.float32) * np.float32(3.0))
+        x[:, [0, 2]] -= np.float32(6.0)          # stop tokens possible but rare
+        x[:, [ord("{"), ord('"'), ord("}")]] += np.float32(5.0)
+        print(f"\n[case] decode loop events step {step}", flush=True)
+        active = dict(loop.active)
+        events = loop.step(_to_dev(t, x))
+        assert set(events) == set(active)
+        for slot in active:
+            st, seq, cfg = ref_state[slot]
+            row = x[slot].copy()
+            if cfg.temperature <= 1e-6:
+                tok = oracle.raw_argmax_host(row)
+            else:
+                eng = oracle.OracleEngine(cfg, _abi, configs_to_array)
+                tok = eng.sample_token(row, st, 10)
+            seq.generated_count += 1
+            want = next_event(seq, tok)
+            assert events[slot] == want, (step, slot)
+        if not loop.active:
+            break
+    loop.close()
