@@ -14,6 +14,15 @@ host-side Python loop cannot issue launches as fast as the GPU runs them).
 
 Prints one JSON line (see `main`). `--gpus N` with N > 1 exits: this build
 runs on one GPU.
+
+Two secondary measurements print their own JSON line instead:
+  --workload decode    one decode step of the scheduler's decode stage for the
+                       config-2 batch (oxs_decode_step: sample, advance, tokens
+                       into host memory), host-observed latency, beside a
+                       device-to-host copy of the tokens and the reference's
+                       copy of the whole logits to the host;
+  --workload dfa_mask  grammar masks (oxs_dfa_mask) for 128 rows over a
+                       128256-token vocabulary.
 """
 from __future__ import annotations
 
@@ -79,7 +88,7 @@ def cpu_baseline(w, gpu_tokens, seconds):
     t0 = time.perf_counter()
     out = run(w.batch)  # warm-up and parity spot check on the whole batch
     t_batch = time.perf_counter() - t0
-    match = bool(np.array_equal(out["tokens"], gpu_tokens))
+    match = bool(np.array_equal(out["tokens"], gpu_tokens)) if gpu_tokens is not None else None
     reps = max(1, int(seconds / max(t_batch, 1e-6)))
     t0 = time.perf_counter()
     for _ in range(reps):
@@ -111,6 +120,178 @@ def cpu_baseline(w, gpu_tokens, seconds):
         "libc": " ".join(platform.libc_ver()),
         "tokens_match_gpu": match,
     }
+
+
+def _percentiles(xs):
+    a = np.sort(np.asarray(xs, dtype=np.float64))
+    return {"median": float(np.median(a)), "p10": float(a[len(a) // 10]), "p90": float(a[(9 * len(a)) // 10])}
+
+
+def bench_decode(args, torch):
+    """Host-observed latency of one decode step over the config-2 batch."""
+    from oxide_sampler import BatchSampler, DecodeLoop, SamplerState  # noqa: PLC0415
+    from oxide_sampler import workloads as wl  # noqa: PLC0415
+
+    d = torch.device("cuda")
+    w = wl.config2()
+    B, V = w.batch, w.vocab
+    H = int(w.history_len[0])
+    n = max(50, args.steps)
+    pool = make_pool(torch, w, 4)
+    loop = DecodeLoop(B, V, history_cap=H + 3 * n + 64)
+    for slot in range(B):
+        st = SamplerState(10.0, w.history[slot, :H].tolist())
+        loop.add_sequence(slot, temperature=w.configs[slot].temperature, top_p=w.configs[slot].top_p,
+                          current_token=1, current_position=H, max_tokens=1 << 30, config=w.configs[slot], state=st)
+
+    def timed(fn, reps):
+        out = []
+        for i in range(reps):
+            t0 = time.perf_counter()
+            fn(i)
+            out.append((time.perf_counter() - t0) * 1e6)
+        return out
+
+    def eager(i):
+        loop.launch(pool[i % len(pool)])
+        loop.wait()
+
+    timed(eager, 20)
+    t_eager = timed(eager, n)
+    static = pool[0].clone()
+    loop.capture(static)
+
+    def replay(i):
+        loop.replay()
+        loop.wait()
+
+    timed(replay, 20)
+    t_graph = timed(replay, n)
+    # GPU time of the step itself, replayed back to back
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(n):
+        loop.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    gpu_us = ev0.elapsed_time(ev1) * 1e3 / n
+    loop.wait()
+
+    # the conventional form: sample, then copy the tokens back and synchronise
+    sampler = BatchSampler(B, V, 256)
+    cfg, _, _, _ = w.packed_configs()
+    d_cfg = torch.from_numpy(cfg).to(d)
+    d_hist = torch.from_numpy(w.history.view(np.int32).copy()).to(d)
+    d_hlen = torch.from_numpy(w.history_len.view(np.int32).copy()).to(d)
+    d_u = torch.from_numpy(w.uniforms).to(d)
+
+    def copy_back(i):
+        out = sampler.sample(pool[i % len(pool)], d_cfg, history=d_hist, history_len=d_hlen, uniforms=d_u)
+        out["tokens"].cpu()
+
+    timed(copy_back, 20)
+    t_copy = timed(copy_back, n)
+    # the reference's hand-off: the whole logits to pinned host memory
+    # (oxide-backend-cuda/src/lib.rs:6037-6041), before any CPU sampling
+    host = torch.empty(B, V, dtype=torch.float32, pin_memory=True)
+
+    def logits_back(i):
+        host.copy_(pool[i % len(pool)], non_blocking=True)
+        torch.cuda.synchronize()
+
+    timed(logits_back, 5)
+    t_logits = timed(logits_back, max(20, n // 10))
+    result = {
+        "metric": "decode step latency, config-2 batch (64 x 128256 f32), sample + advance + tokens on the host",
+        "value": _percentiles(t_graph)["median"],
+        "unit": "us/step",
+        "higher_is_better": False,
+        "n_gpus": 1,
+        "steps": n,
+        "dtype": "f32",
+        "data": "synthetic (config-2 batch and 3 GPU-drawn batches of the same distribution)",
+        "config": {"workload": "decode: 64 sequences, config-2 SamplingConfig and a 512-token history each, "
+                               "device xorshift draws; DecodeLoop over oxs_decode_step"},
+        "graph_replay_us": _percentiles(t_graph),
+        "eager_launch_us": _percentiles(t_eager),
+        "gpu_us_per_step": gpu_us,
+        "sample_then_copy_tokens_us": _percentiles(t_copy),
+        "reference_logits_to_host_us": _percentiles(t_logits),
+        "reference_logits_bytes": B * V * 4,
+    }
+    if not args.no_cpu:
+        base = cpu_baseline(w, None, args.cpu_seconds)
+        base["note"] = "CPU sampling the reference runs after the logits copy, per step, rows in series"
+        base["us_per_step"] = base["us_per_row"] * B
+        result["cpu_baseline"] = base
+    print(json.dumps(result), flush=True)
+    loop.close()
+
+
+def bench_dfa_mask(args, torch):
+    """oxs_dfa_mask over 128 rows x a 128256-token synthetic vocabulary."""
+    from oxide_sampler import DfaSchemaGrammar, TokenBytes  # noqa: PLC0415
+
+    B, V = 128, 128256
+    rng = np.random.default_rng(0x5EED00DF)
+    alphabet = np.frombuffer(b'{}[]":,0123456789abcdefghijklmnopqrstuvwxyz _-.', np.uint8)
+    lens = np.minimum(rng.geometric(0.25, size=V), 24)  # mean ~4 bytes, a few long tokens
+    vocab = [bytes(alphabet[rng.integers(0, alphabet.shape[0], size=int(L))]) for L in lens]
+    tb = TokenBytes(vocab)
+    grammars = {"json_validator_8_states": DfaSchemaGrammar.new_simple_json_validator(),
+                "fixed_prefix_68_states": DfaSchemaGrammar.new_json_with_fixed_prefix('{"' + "k" * 60 + '": ')}
+    n = max(20, args.steps // 10)
+    lines = {}
+    for name, g in grammars.items():
+        states = rng.integers(0, g.num_states, size=B).astype(np.uint32)
+        d_states = torch.from_numpy(states.view(np.int32)).cuda()
+        for _ in range(5):
+            g.token_masks(tb, d_states)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(n):
+            g.token_masks(tb, d_states)
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / n
+        lookups = float(B) * float(lens.sum())  # upper bound: every walk runs to the token's end
+        lines[name] = {"us_per_call": us, "rows": B, "vocab": V, "states": g.num_states,
+                       "token_bytes": int(lens.sum()), "row_token_pairs_per_s": B * V / (us * 1e-6),
+                       "table_lookups_upper_bound_per_s": lookups / (us * 1e-6),
+                       "table": "LDS" if g.num_states <= 48 else "global (L2)"}
+    result = {
+        "metric": "grammar mask latency, 128 rows x 128256-token vocabulary",
+        "value": lines["json_validator_8_states"]["us_per_call"],
+        "unit": "us/call",
+        "higher_is_better": False,
+        "n_gpus": 1,
+        "steps": n,
+        "dtype": "u8/u32",
+        "data": "synthetic vocabulary (geometric token lengths, mean 4 bytes, JSON-ish alphabet), random states",
+        "config": {"workload": "dfa_mask: oxs_dfa_mask, 128 rows, V=128256"},
+        "grammars": lines,
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oxs_oracle_ctypes as oracle  # noqa: PLC0415 — baseline leg only
+
+        g = grammars["json_validator_8_states"]
+        offsets = tb.offsets.cpu().numpy().view(np.uint32)
+        flat = tb.bytes.cpu().numpy()[: tb.num_bytes]
+        rows = 8
+        states = rng.integers(0, g.num_states, size=rows).astype(np.uint32)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < args.cpu_seconds or reps == 0:
+            oracle.dfa_mask_host(g.transitions, g.num_states, offsets, flat, states)
+            reps += 1
+        dt = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": reps * rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                                  "sample": f"{reps} x {rows} rows of the 8-state grammar over the same vocabulary",
+                                  "us_per_call_128_rows": dt / (reps * rows) * 128 * 1e6}
+    print(json.dumps(result), flush=True)
 
 
 def read_traffic(path):
@@ -189,6 +370,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only 8 plain 256 MiB device copies (scale for the rocprofv3 byte counters)")
     ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
+    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask"), default="sample",
+                    help="sample: the headline config-2 line; decode / dfa_mask: secondary measurements")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="turn four rocprofv3 --pmc output folders into the traffic summary and exit")
     args = ap.parse_args()
@@ -212,6 +395,12 @@ def main():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(1)
     d = torch.device("cuda")
+    if args.workload == "decode":
+        bench_decode(args, torch)
+        return
+    if args.workload == "dfa_mask":
+        bench_dfa_mask(args, torch)
+        return
     if args.calibrate_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device=d)  # 256 MiB
         dst = torch.empty_like(src)

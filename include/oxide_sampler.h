@@ -221,8 +221,9 @@ typedef struct oxs_decode_io {
   int32_t* current_position;  /* [B] += 1 (:975) */
   uint32_t* generated_count;  /* [B] += 1 (:976) */
   /* Host memory from oxs_host_alloc (megakernel_ops.cu:331-347's h_sampled_token):
-   * host_tokens[B] receives the tokens and *host_seq is incremented once every
-   * row's host token is visible, so the host can poll it instead of
+   * host_tokens[B] receives the tokens and, once every row's host token is
+   * visible, *host_seq receives the number of steps with host_seq set that
+   * this sampler has completed, so the host can poll it instead of
    * synchronising the stream. */
   uint32_t* host_tokens;
   uint32_t* host_seq;

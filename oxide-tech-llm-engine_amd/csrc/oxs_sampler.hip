@@ -106,7 +106,7 @@ struct Params {
   uint32_t* dec_count;    // [B] generated count
   uint32_t* host_tokens;  // [B] host memory
   uint32_t* host_seq;     // host memory: completed steps
-  uint32_t* ticket;       // rows finished in this launch (0 between launches)
+  uint32_t* ticket;       // [0] rows finished in this launch (0 between launches), [1] steps published
 };
 
 // ---------------------------------------------------------------- keys
@@ -1111,26 +1111,43 @@ __device__ __forceinline__ Chain seq_chain(const float* a, uint32_t n, float ini
   return Chain{n, s, false};
 }
 
+// Per-row values the chain and the decode step need from global memory, read
+// at tail start.
+struct RowState {
+  float uniform;
+  float mu;
+  uint64_t rng;
+  uint32_t history_len;
+  bool raw;            // a raw decode row: no history, no candidates buffer
+  int32_t dec_pos;     // decode step: the row's position and generated count
+  uint32_t dec_count;
+};
+
 // The decode loop's bookkeeping once a row's token is known, by the thread
 // that wrote it (continuous_batching.rs:974-976; the device-side advance and
 // host hand-off of megakernel_ops.cu:331-347): the next step's input token,
 // position and generated count, the token in host memory and, from the row
 // that finishes last, the host's step counter, released after every row's
 // host token.
-__device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, uint32_t token) {
+__device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, uint32_t token, const RowState& rs) {
   if (!(p.flags & kFlagDecode)) return;
   if (p.dec_token) p.dec_token[row] = token;
-  if (p.dec_pos) p.dec_pos[row] += 1;
-  if (p.dec_count) p.dec_count[row] += 1u;
-  if (p.host_tokens) p.host_tokens[row] = token;
+  if (p.dec_pos) p.dec_pos[row] = rs.dec_pos + 1;
+  if (p.dec_count) p.dec_count[row] = rs.dec_count + 1u;
+  // The host token is a system-scope store (written through to host memory);
+  // the ticket is a release at agent scope, so no row invalidates its L2. The
+  // row that takes the last ticket acquires every row's release, counts the
+  // step in device memory and publishes the count with one system-scope
+  // release (ticket[0]: rows done in this launch; ticket[1]: steps done).
+  if (p.host_tokens) __hip_atomic_store(p.host_tokens + row, token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   if (p.host_seq) {
-    __threadfence_system();  // this row's host token before its ticket
-    const uint32_t done = __hip_atomic_fetch_add(p.ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == p.B - 1u) {  // the last row: every other row's host token is visible
+    const uint32_t done = __hip_atomic_fetch_add(p.ticket, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == p.B - 1u) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __threadfence_system();
-      const uint32_t n = __hip_atomic_load(p.host_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      __hip_atomic_store(p.host_seq, n + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      const uint32_t n = __hip_atomic_load(p.ticket + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+      __hip_atomic_store(p.ticket + 1, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.host_seq, n, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
 }
@@ -1138,12 +1155,12 @@ __device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, ui
 // A row that ends before the chain. A raw decode row leaves the caller's
 // candidates buffer as it was.
 __device__ __forceinline__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status,
-                                                 bool raw) {
+                                                 const RowState& rs) {
   if (threadIdx.x == 0) {
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
-    if (p.out_kept_count && !raw) p.out_kept_count[row] = 0;
-    decode_advance(p, row, token);
+    if (p.out_kept_count && !rs.raw) p.out_kept_count[row] = 0;
+    decode_advance(p, row, token, rs);
   }
 }
 
@@ -1159,14 +1176,6 @@ struct ChainBufs {
   float* hit;  // 16 floats
 };
 
-// Per-row values the chain needs from global memory, read at tail start.
-struct RowState {
-  float uniform;
-  float mu;
-  uint64_t rng;
-  uint32_t history_len;
-  bool raw;  // a raw decode row: no history, no candidates buffer
-};
 
 // Stable in-place compaction of (ids, pr)[0..len) by one wavefront: a step
 // reads 4 x 64 entries, keeps those with keep(v), and writes them below the
@@ -1426,7 +1435,7 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
     if (p.out_kept_count && !rs.raw) p.out_kept_count[row] = len;
-    decode_advance(p, row, token);
+    decode_advance(p, row, token, rs);
   }
   const uint32_t nk = rs.raw ? 0u : (uint32_t)min((int64_t)len, p.kept_ld);
   for (uint32_t i = l; i < nk; i += 64) {
@@ -1632,17 +1641,20 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   rs.rng = rin.rng;
   rs.history_len = rin.history_len;
   rs.raw = rin.raw;
+  const bool dec = (p.flags & kFlagDecode) != 0;
+  rs.dec_pos = dec && p.dec_pos ? p.dec_pos[row] : 0;
+  rs.dec_count = dec && p.dec_count ? p.dec_count[row] : 0u;
   store_libm_tables(tabv, s_tab);
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
 
 
   const uint32_t M = max(c.top_k, 256u);
   if (M > (uint32_t)kMaxM || (r.dry && min(r.hlen, r.dry_range) > (uint32_t)kDryMax)) {
-    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED, rin.raw);  // sizes this build does not run on the device
+    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // sizes this build does not run on the device
     return;
   }
   if (c.mirostat_mode != OXS_MIROSTAT_DISABLED && !p.mu) {
-    write_row_result(p, row, 0u, OXS_ROW_MISSING_STATE, rin.raw);
+    write_row_result(p, row, 0u, OXS_ROW_MISSING_STATE, rs);
     return;
   }
   // DRY rows: their values, then the exact path (the stream kernel's
@@ -1745,7 +1757,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
 
   if (path == 0) {
     if (meff == 0) {  // every logit -inf or NaN (:267-270)
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rin.raw);
+      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
       return;
     }
     const uint32_t span_k = s_bstart[last] + s_bcount[last];  // keys in buckets 0 .. last
@@ -1777,7 +1789,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     } else {
       meff = min(M, N);
       if (meff == 0) {
-        write_row_result(p, row, 0u, OXS_ROW_EMPTY, rin.raw);
+        write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
         return;
       }
       keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
@@ -1786,7 +1798,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   if (path == 2) {
     meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)s_keys, s_bcount, s_top, ts);
     if (meff == 0) {
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rin.raw);
+      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
       return;
     }
     bitonic_sort<false>(s_top, meff);
@@ -1896,7 +1908,7 @@ struct oxs_sampler {
   uint64_t* libm;
   uint64_t* dry_list;
   uint32_t* dry_count;
-  uint32_t* ticket;  // decode steps: rows finished in the running launch
+  uint32_t* ticket;  // decode steps: rows finished in the running launch, steps published
   size_t bytes;
 };
 
