@@ -291,6 +291,21 @@ typedef struct oxs_token_bytes {
 int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, const uint32_t* states, uint32_t batch,
                  uint32_t* mask, int64_t mask_ld, void* stream);
 
+/*
+ * Grammar masks by state. A token's walk depends only on the state it starts
+ * from, so the masks of a grammar over a vocabulary can be computed once, with
+ * oxs_dfa_mask over the states 0 .. num_states (the last one stands for every
+ * state outside the table, from which only tokens with no bytes are allowed),
+ * into state_masks[(num_states + 1) * state_masks_ld] words, and each step's
+ * masks then gathered: row b of `mask` is row min(states[b], num_states) of
+ * state_masks. The result equals oxs_dfa_mask on the same states.
+ * Asynchronous on `stream`; allocates nothing. Returns
+ * OXS_ERR_INVALID_ARGUMENT for missing pointers, a leading dimension below
+ * ceil(vocab / 32) or batch above 65535.
+ */
+int oxs_dfa_mask_gather(const uint32_t* state_masks, uint32_t num_states, int64_t state_masks_ld, uint32_t vocab,
+                        const uint32_t* states, uint32_t batch, uint32_t* mask, int64_t mask_ld, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

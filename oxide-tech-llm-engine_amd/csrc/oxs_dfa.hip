@@ -12,6 +12,11 @@
 // lookups bound this kernel, not HBM (the token bytes and offsets are read once
 // per row group). A wavefront's 64 consecutive tokens give two mask words per
 // row from one ballot.
+//
+// A walk depends only on the state it starts from, so a decode loop computes
+// the masks of every state once per grammar and vocabulary (this kernel over
+// the states themselves) and gathers one row per sequence each step
+// (mask_gather_kernel): a copy of ceil(V / 32) words per row.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -116,6 +121,25 @@ __global__ __launch_bounds__(kThreads) void dfa_mask_kernel(const Params p) {
   }
 }
 
+// Row b of the output is row min(states[b], num_states) of the per-state
+// masks (row num_states holds the masks of every state outside the table).
+constexpr int kGatherWords = 4 * kThreads;  // words per gather block
+__global__ __launch_bounds__(kThreads) void mask_gather_kernel(const uint32_t* __restrict__ table, uint32_t num_states,
+                                                              int64_t table_ld, uint32_t words,
+                                                              const uint32_t* __restrict__ states,
+                                                              uint32_t* __restrict__ mask, int64_t mask_ld) {
+  const uint32_t row = blockIdx.y;
+  const uint32_t s = min(states[row], num_states);
+  const uint32_t* src = table + (size_t)s * table_ld;
+  uint32_t* dst = mask + (size_t)row * mask_ld;
+  const uint32_t w0 = blockIdx.x * kGatherWords;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t w = w0 + k * kThreads + threadIdx.x;
+    if (w < words) dst[w] = src[w];
+  }
+}
+
 }  // namespace oxs_grammar
 
 extern "C" int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, const uint32_t* states,
@@ -147,5 +171,20 @@ extern "C" int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, c
     hipLaunchKernelGGL(dfa_mask_kernel<true>, grid, dim3(kThreads), p.num_states * 256u * sizeof(uint32_t), st, p);
   else
     hipLaunchKernelGGL(dfa_mask_kernel<false>, grid, dim3(kThreads), 0, st, p);
+  return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+}
+
+extern "C" int oxs_dfa_mask_gather(const uint32_t* state_masks, uint32_t num_states, int64_t state_masks_ld,
+                                   uint32_t vocab, const uint32_t* states, uint32_t batch, uint32_t* mask,
+                                   int64_t mask_ld, void* stream) {
+  using namespace oxs_grammar;
+  if (batch == 0 || vocab == 0) return OXS_OK;
+  const uint32_t words = (vocab + 31u) / 32u;
+  if (!state_masks || !states || !mask || state_masks_ld < (int64_t)words || mask_ld < (int64_t)words)
+    return OXS_ERR_INVALID_ARGUMENT;
+  if (batch > 65535u) return OXS_ERR_INVALID_ARGUMENT;  // one grid row per batch row
+  const dim3 grid((words + kGatherWords - 1) / kGatherWords, batch);
+  hipLaunchKernelGGL(mask_gather_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, state_masks, num_states,
+                     state_masks_ld, words, states, mask, mask_ld);
   return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }

@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "oxs_host_alloc",
     "oxs_host_free",
     "oxs_dfa_mask",
+    "oxs_dfa_mask_gather",
 )
 
 OXS_DFA_ERROR_STATE = 0xFFFFFFFF
@@ -201,6 +202,10 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_dfa_mask.restype = ctypes.c_int
     lib.oxs_dfa_mask.argtypes = [ctypes.POINTER(OxsDfa), ctypes.POINTER(OxsTokenBytes), ctypes.c_void_p,
                                  ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    lib.oxs_dfa_mask_gather.restype = ctypes.c_int
+    lib.oxs_dfa_mask_gather.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int64, ctypes.c_uint32,
+                                        ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64,
+                                        ctypes.c_void_p]
     if lib.oxs_abi_version() != OXS_ABI_VERSION:
         raise RuntimeError(f"liboxide_sampler ABI {lib.oxs_abi_version()} != {OXS_ABI_VERSION}")
     if path is None:

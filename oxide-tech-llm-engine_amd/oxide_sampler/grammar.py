@@ -9,7 +9,10 @@ crates/oxide-server/src/dfa.rs). Its token masks run on the GPU through
   masks for a batch of rows, ready for `oxs_sample_batch`'s allowed_mask
   (StructuredOutputEngine::compute_token_mask, grammar_engine.rs:42-65);
 - `DfaSchemaGrammar.apply_dfa_mask(state, vocab_bytes, logits)`: the reference's
-  in-place -inf masking of one row (dfa.rs:130-148).
+  in-place -inf masking of one row (dfa.rs:130-148);
+- `DfaSchemaGrammar.state_masks(token_bytes)` then `.gather_masks(compiled,
+  states)`: the same masks from a per-state table computed once per grammar and
+  vocabulary (`oxs_dfa_mask_gather`), for decode loops.
 
 `transition`, `deterministic_transition` and `find_jump_forward_bytes` walk the
 table on the host, as the reference does (dfa.rs:110-190): they are single
@@ -63,6 +66,17 @@ class TokenBytes:
 
     def as_c(self) -> OxsTokenBytes:
         return OxsTokenBytes(self.vocab, self.num_bytes, self.offsets.data_ptr(), self.bytes.data_ptr())
+
+
+class StateMasks:
+    """Packed masks of every state of one grammar over one vocabulary:
+    `table` is int32 [num_states + 1, ceil(vocab / 32)] on the GPU."""
+
+    def __init__(self, num_states: int, vocab: int, table):
+        self.num_states = int(num_states)
+        self.vocab = int(vocab)
+        self.words = (self.vocab + 31) // 32
+        self.table = table
 
 
 class DfaSchemaGrammar:
@@ -174,6 +188,34 @@ class DfaSchemaGrammar:
                                ctypes.c_void_p(mask.data_ptr()), mask.stride(0), ctypes.c_void_p(s.cuda_stream)),
               "oxs_dfa_mask")
         return mask[:, :words]
+
+    def state_masks(self, token_bytes: TokenBytes, device: int = 0, stream=None) -> "StateMasks":
+        """The masks of every state, once: rows 0 .. num_states - 1, and row
+        num_states for any state outside the table."""
+        t = _torch()
+        states = t.arange(self.num_states + 1, dtype=t.int32, device=t.device("cuda", device))
+        m = self.token_masks(token_bytes, states, device, stream)
+        return StateMasks(self.num_states, token_bytes.vocab, m.contiguous())
+
+    def gather_masks(self, compiled: "StateMasks", states, out=None, device: int = 0, stream=None):
+        """token_masks(states) from a StateMasks table (int32 [len(states), ceil(vocab / 32)])."""
+        t = _torch()
+        lib = load_library()
+        if compiled.num_states != self.num_states:
+            raise ValueError("the table was compiled for another grammar")
+        dev = t.device("cuda", device)
+        st = states if hasattr(states, "data_ptr") else t.tensor(np.asarray(states, np.uint32).view(np.int32), device=dev)
+        st = st.to(dev).contiguous()
+        B = int(st.shape[0])
+        words = compiled.words
+        if out is None:
+            out = t.empty(B, max(words, 1), dtype=t.int32, device=dev)
+        s = stream if stream is not None else t.cuda.current_stream(dev)
+        check(lib.oxs_dfa_mask_gather(ctypes.c_void_p(compiled.table.data_ptr()), self.num_states,
+                                      compiled.table.stride(0), compiled.vocab, ctypes.c_void_p(st.data_ptr()), B,
+                                      ctypes.c_void_p(out.data_ptr()), out.stride(0), ctypes.c_void_p(s.cuda_stream)),
+              "oxs_dfa_mask_gather")
+        return out[:, :words]
 
     def apply_dfa_mask(self, current_state: int, token_bytes, logits) -> None:
         """dfa.rs:130-148: tokens whose bytes do not walk from current_state get -inf (in place)."""

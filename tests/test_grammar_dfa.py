@@ -208,3 +208,26 @@ def test_gpu_dfa_mask_feeds_the_sampler(torch_gpu):
             s = int(states[b])
             for byte in vocab[t]:
                 s = dfa.transition(s, byte)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,V", [(8, 1000), (47, 4097), (70, 20000)])
+def test_gpu_state_mask_gather_matches_direct_walk(torch_gpu, n, V):
+    # per-state masks computed once, gathered per step: equal to the direct walk and the oracle
+    from oxide_sampler.grammar import TokenBytes
+    rng = np.random.default_rng(n + V)
+    table = random_dfa(rng, n, 0.4)
+    vocab = random_vocab(rng, V, JSON_ALPHA, 6)
+    g = DfaSchemaGrammar(n, table, [False] * n)
+    tb = TokenBytes(vocab)
+    print(f"\n[case] state-mask gather states={n} vocab={V}", flush=True)
+    compiled = g.state_masks(tb)
+    off, by = pack(vocab)
+    for step in range(3):
+        states = rng.integers(0, n, size=37).astype(np.uint32)
+        states[::7] = n + 3
+        states[5] = ERR
+        got = g.gather_masks(compiled, states).cpu().numpy().view(np.uint32)
+        direct = g.token_masks(tb, states).cpu().numpy().view(np.uint32)
+        np.testing.assert_array_equal(got, direct)
+        np.testing.assert_array_equal(got, oracle.dfa_mask_host(table, n, off, by, states))
