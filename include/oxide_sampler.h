@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define OXS_ABI_VERSION 2u
+#define OXS_ABI_VERSION 3u
 
 /* Return codes. EngineError (crates/oxide-core/src/error.rs:6) has one variant
  * on this path, ShapeMismatch (error.rs:52; sampler.rs:179-181). */
@@ -160,6 +160,14 @@ typedef struct oxs_batch {
    * overlap `logits`. */
   float* logits_out;
   int64_t logits_out_ld;
+
+  /* The model's final logit softcap (final_logit_softcapping), done by the
+   * reference as a pass of its own over the logits before sampling
+   * (oxide-backend-cuda/src/lib.rs:3243-3255, launch_cuda_logit_softcap,
+   * kernels/vec_ops_activations.cu:131-136). When > 0, every logit becomes
+   * cap * tanhf(logit / cap) as it is read, before the mask and every
+   * sampler stage; tanhf is glibc's (Rust's f32::tanh). 0 (or NaN) = off. */
+  float logit_softcap;
 } oxs_batch;
 
 typedef struct oxs_sampler oxs_sampler;

@@ -401,6 +401,10 @@ static int batch_rows(const oxs_batch* b, const oxs_decode_io* dec, int n_thread
         const float* src = (const float*)b->logits + (size_t)r * b->logits_ld;
         memcpy(row.data(), src, sizeof(float) * b->vocab);
       }
+      if (b->logit_softcap > 0.0f) {  // lib.rs:3243-3255 / vec_ops_activations.cu:131-136, before sampling
+        const float cap = b->logit_softcap;
+        for (uint32_t i = 0; i < b->vocab; ++i) row[i] = cap * tanhf(row[i] / cap);
+      }
       if (b->allowed_mask) {
         const uint32_t* m = b->allowed_mask + (size_t)r * b->mask_ld;
         for (uint32_t i = 0; i < b->vocab; ++i)

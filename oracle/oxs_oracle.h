@@ -57,8 +57,9 @@ int oxo_sample_token(const oxs_sampling_config* cfg, const uint32_t* bias_ids,
 
 /*
  * The same descriptor as oxs_sample_batch, with HOST pointers, sampled row by
- * row (the packed mask is applied first by writing -inf, as the reference's
- * grammar maskers do). Logits are copied per row, so the input is not
+ * row (a logit softcap first, cap * tanhf(l / cap) with the platform tanhf as
+ * the backend's softcap pass does before sampling; then the packed mask by
+ * writing -inf, as the reference's grammar maskers do). Logits are copied per row, so the input is not
  * modified. n_threads > 1 splits rows statically over that many threads.
  * Returns 0 or OXO_SHAPE_MISMATCH.
  */

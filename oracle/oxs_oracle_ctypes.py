@@ -67,7 +67,7 @@ def _ptr(a):
 
 def sample_batch_host(abi, *, logits, dtype, configs_bytes, bias_ids, bias_values, ban_ids, mask, history,
                       history_len, history_cap, record, uniforms, rng_state, mu, kept_ld, logits_out=None,
-                      shared_config=False, n_threads=1, decode=None, kept_fill=0):
+                      shared_config=False, n_threads=1, decode=None, kept_fill=0, softcap=0.0):
     """Runs the oracle over host numpy arrays with the oxs_batch descriptor.
 
     `abi` is the product's ctypes module (for the OxsBatch layout). Mutable
@@ -116,6 +116,7 @@ def sample_batch_host(abi, *, logits, dtype, configs_bytes, bias_ids, bias_value
     if logits_out is not None:
         b.logits_out = logits_out.ctypes.data
         b.logits_out_ld = logits_out.shape[1]
+    b.logit_softcap = softcap
     if decode is None:
         rc = lib.oxo_sample_batch(ctypes.byref(b), n_threads)
     else:

@@ -1,6 +1,6 @@
-// Single-precision exp/ln/log2/pow that reproduce, bit for bit, the glibc >= 2.27
-// implementations that Rust's f32::{exp, ln, log2, powf} lower to on
-// x86_64-linux-gnu.
+// Single-precision exp/ln/log2/pow (and tanh, at the end) that reproduce, bit
+// for bit, the glibc >= 2.27 implementations that Rust's f32::{exp, ln, log2,
+// powf, tanh} lower to on x86_64-linux-gnu.
 //
 // The reference sampler (crates/oxide-core/src/sampler.rs:289 exp, :424 and
 // :440/:451 log2, :496/:502 ln, :409 powf) calls the platform libm. glibc's single
@@ -307,6 +307,115 @@ OXS_HD float powf_t(float x, float y, const uint64_t* exp2tab = kExp2Tab, const 
     if (ylogx <= -150.0) return sign_bias ? -0.0f : 0.0f;                                         // underflow
   }
   return (float)powf_exp2<FUSED>(ylogx, sign_bias, exp2tab);
+}
+
+// ---------------------------------------------------------------- tanhf
+
+// glibc's single-precision tanh and expm1 (sysdeps/ieee754/flt-32/s_tanhf.c
+// and s_expm1f.c, the Sun fdlibm algorithms in float arithmetic): Rust's
+// f32::tanh on x86_64-linux-gnu, used for the logit softcap cap * tanh(l / cap)
+// (oxide-backend-cuda/src/kernels/vec_ops_activations.cu:131-136). The
+// operations are plain IEEE float steps, so no fused form exists; the host
+// glibc agrees with this restatement on every one of the 2^32 inputs.
+//
+// expm1f: x = k ln2 + r with |r| <= ln2 / 2 (ln2 split into a high part exact
+// in products with k and a low part), expm1(r) from a degree-5 rational
+// correction in r^2 / 2, then rescaled by 2^k.
+OXS_HD float expm1f_fdlibm(float x) {
+  const float one = 1.0f, huge = 1.0e+30f, tiny = 1.0e-30f;
+  const float o_threshold = u2f(0x42b17180u), ln2_hi = u2f(0x3f317180u), ln2_lo = u2f(0x3717f7d1u),
+              invln2 = u2f(0x3fb8aa3bu);
+  const float Q1 = u2f(0xbd088889u), Q2 = u2f(0x3ad00d01u), Q3 = u2f(0xb8a670cdu), Q4 = u2f(0x36867e54u),
+              Q5 = u2f(0xb457edbbu);
+  float y, hi, lo, c = 0.0f, t, e, hxs, hfx, r1;
+  int32_t k;
+  uint32_t hx = f2u(x);
+  const uint32_t xsb = hx & 0x80000000u;
+  hx &= 0x7fffffffu;
+  if (hx >= 0x4195b844u) {    // |x| >= 27 ln2
+    if (hx >= 0x42b17218u) {  // |x| >= 88.72...
+      if (hx > 0x7f800000u) return x + x;                 // NaN
+      if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;  // exp(+-inf) - 1
+      if (x > o_threshold) return huge * huge;            // overflow
+    }
+    if (xsb != 0) return tiny - one;  // x < -27 ln2: -1
+  }
+  if (hx > 0x3eb17218u) {    // |x| > ln2 / 2: reduce
+    if (hx < 0x3f851592u) {  // and |x| < 3 ln2 / 2
+      if (xsb == 0) {
+        hi = x - ln2_hi;
+        lo = ln2_lo;
+        k = 1;
+      } else {
+        hi = x + ln2_hi;
+        lo = -ln2_lo;
+        k = -1;
+      }
+    } else {
+      k = (int32_t)(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
+      t = (float)k;
+      hi = x - t * ln2_hi;  // exact
+      lo = t * ln2_lo;
+    }
+    x = hi - lo;
+    c = (hi - x) - lo;
+  } else if (hx < 0x33000000u) {  // |x| < 2^-25: x
+    t = huge + x;
+    return x - (t - (huge + x));
+  } else {
+    k = 0;
+  }
+  hfx = 0.5f * x;
+  hxs = x * hfx;
+  r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+  t = 3.0f - r1 * hfx;
+  e = hxs * ((r1 - t) / (6.0f - x * t));
+  if (k == 0) return x - (x * e - hxs);
+  e = (x * (e - c) - c);
+  e -= hxs;
+  if (k == -1) return 0.5f * (x - e) - 0.5f;
+  if (k == 1) {
+    if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+    return one + 2.0f * (x - e);
+  }
+  if (k <= -2 || k > 56) {  // exp(x) - 1 from exp(x)
+    y = one - (e - x);
+    if (k == 128) y = y * 2.0f * 0x1p127f;
+    else y = u2f(f2u(y) + ((uint32_t)k << 23));
+    return y - one;
+  }
+  if (k < 23) {
+    t = u2f(0x3f800000u - (0x1000000u >> k));  // 1 - 2^-k
+    y = t - (e - x);
+  } else {
+    t = u2f((uint32_t)(0x7f - k) << 23);  // 2^-k
+    y = x - (e + t);
+    y += one;
+  }
+  return u2f(f2u(y) + ((uint32_t)k << 23));
+}
+
+// tanh(x) = 1 - 2 / (expm1(2|x|) + 2) for |x| >= 1, -t / (t + 2) with
+// t = expm1(-2|x|) below, x(1 + x) for |x| < 2^-55, +-1 from |x| >= 22.
+OXS_HD float tanhf_fdlibm(float x) {
+  const float one = 1.0f, two = 2.0f, tiny = 1.0e-30f;
+  float t, z;
+  const uint32_t jx = f2u(x), ix = jx & 0x7fffffffu;
+  if (ix >= 0x7f800000u) return (jx >> 31) == 0 ? one / x + one : one / x - one;  // +-inf: +-1; NaN
+  if (ix < 0x41b00000u) {  // |x| < 22
+    if (ix == 0) return x;
+    if (ix < 0x24000000u) return x * (one + x);
+    if (ix >= 0x3f800000u) {
+      t = expm1f_fdlibm(two * (jx >> 31 ? -x : x));
+      z = one - two / (t + two);
+    } else {
+      t = expm1f_fdlibm(-two * (jx >> 31 ? -x : x));
+      z = -t / (t + two);
+    }
+  } else {
+    z = one - tiny;
+  }
+  return (jx >> 31) == 0 ? z : -z;
 }
 
 }  // namespace oxs_libm

@@ -61,6 +61,15 @@ constexpr uint32_t kNlFlag = 1u << 30;
 constexpr uint32_t kDryFlag = 1u << 31;  // exact-path table: the id has a DRY value
 constexpr uint32_t kFlagDecode = 1u << 31;  // Params.flags: a decode step (oxs_decode_step)
 
+// Kernel kinds (the DT template argument): the logit dtype (OXS_DTYPE_*) plus
+// compile-time features, so that launches without a feature carry none of its
+// code.
+constexpr int kKindSoftcap = 4;  // logits pass through the softcap as they are read
+constexpr int kKindDecode = 8;   // tail only: the decode step's bookkeeping
+constexpr bool kind_f32(int k) { return (k & 3) == OXS_DTYPE_F32; }
+constexpr bool kind_softcap(int k) { return (k & kKindSoftcap) != 0; }
+constexpr bool kind_decode(int k) { return (k & kKindDecode) != 0; }
+
 struct Params {
   const void* logits;
   int64_t ld;
@@ -86,6 +95,7 @@ struct Params {
   int64_t kept_ld;
   float* logits_out;
   int64_t logits_out_ld;
+  float softcap;  // > 0: logits become softcap * tanh(logit / softcap) as they are read
   // geometry
   uint32_t S;      // chunks per row
   uint32_t CH;     // logits per chunk
@@ -216,14 +226,25 @@ __device__ __forceinline__ float apply_special(const uint32_t* bias_ids, const f
   return special_post(r, special_pre(bias_ids, bias_values, r, x, entry, idx), entry);
 }
 
+// The model's final logit softcap (oxide-backend-cuda/src/lib.rs:3243-3255,
+// kernels/vec_ops_activations.cu:131-136), applied to each logit as it is
+// read instead of in a pass of its own: cap * tanh(l / cap), with glibc's
+// tanhf. Only the softcap kinds of the kernels contain it.
+__device__ __forceinline__ float softcap_of(float x, float cap) {
+  return cap * oxs_libm::tanhf_fdlibm(x / cap);
+}
+
 template <int DT>
 __device__ __forceinline__ float load_logit(const Params& p, uint32_t row, uint32_t idx) {
-  if constexpr (DT == OXS_DTYPE_F32) {
-    return ((const float*)p.logits)[(size_t)row * p.ld + idx];
+  float x;
+  if constexpr (kind_f32(DT)) {
+    x = ((const float*)p.logits)[(size_t)row * p.ld + idx];
   } else {
     const uint16_t b = ((const uint16_t*)p.logits)[(size_t)row * p.ld + idx];
-    return __uint_as_float((uint32_t)b << 16);
+    x = __uint_as_float((uint32_t)b << 16);
   }
+  if constexpr (kind_softcap(DT)) return softcap_of(x, p.softcap);
+  return x;
 }
 
 __device__ __forceinline__ bool mask_allows(const Params& p, uint32_t row, uint32_t idx) {
@@ -486,10 +507,10 @@ __device__ __forceinline__ void unit_of(const Params& p, uint32_t* row, uint32_t
 // scale, and a row with any other scale is sent to the tail's exact path.
 template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
 __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint32_t chunk, const RowXf& r,
-                                             const uint32_t (&raw)[SLOTS][(DT == OXS_DTYPE_F32) ? 4 : 8],
+                                             const uint32_t (&raw)[SLOTS][kind_f32(DT) ? 4 : 8],
                                              const uint32_t (&mw)[SLOTS], float* s_x, uint32_t* s_hkeys,
                                              uint32_t* s_hvals, uint32_t* s_full) {
-  constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;
+  constexpr int EPL = kind_f32(DT) ? 4 : 8;
   constexpr int TILE = kThreads * EPL;
   constexpr int NE = SLOTS * EPL;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -667,12 +688,12 @@ __device__ __forceinline__ void build_marks(const Params& p, const RowXf& r, uin
 // second half is still in flight.
 template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
 __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
-  constexpr int EPL = (DT == OXS_DTYPE_F32) ? 4 : 8;  // logits per 16-byte load
+  constexpr int EPL = kind_f32(DT) ? 4 : 8;  // logits per 16-byte load
   constexpr int TILE = kThreads * EPL;
   constexpr int CH = SLOTS * TILE;
   constexpr int NE = SLOTS * EPL;  // logits per lane
   constexpr int H1 = (SLOTS + 1) / 2;  // loads issued before the row's record is read
-  constexpr size_t ESZ = (DT == OXS_DTYPE_F32) ? 4 : 2;
+  constexpr size_t ESZ = kind_f32(DT) ? 4 : 2;
   static_assert(CH <= kMaxChunk, "chunk too large");
   static_assert(NE <= 32, "one survivor bit per logit of a lane");
 
@@ -697,7 +718,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
       // last group (in bounds) and their values are dropped later.
       const uint32_t at = base < c1 ? base : p.V - EPL;
       const u32x4 q = __builtin_nontemporal_load((const u32x4*)(rowp + (size_t)at * ESZ));
-      if constexpr (DT == OXS_DTYPE_F32) {
+      if constexpr (kind_f32(DT)) {
         raw[s][0] = q.x; raw[s][1] = q.y; raw[s][2] = q.z; raw[s][3] = q.w;
       } else {
         raw[s][0] = q.x << 16; raw[s][1] = q.x & 0xffff0000u;
@@ -745,6 +766,12 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
 #pragma unroll
   for (int s = H1; s < SLOTS; ++s) load_slot(s);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kind_softcap(DT) && VEC) {  // (the scalar loads above went through load_logit)
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) raw[s][e] = __float_as_uint(softcap_of(__uint_as_float(raw[s][e]), p.softcap));
+  }
   if (r.any_special) {
     __syncthreads();  // tables cleared
     build_marks(p, r, row, c0, c1, hv, s_hkeys, s_hvals, &s_full);
@@ -1129,8 +1156,9 @@ struct RowState {
 // position and generated count, the token in host memory and, from the row
 // that finishes last, the host's step counter, released after every row's
 // host token.
+template <int DT>
 __device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, uint32_t token, const RowState& rs) {
-  if (!(p.flags & kFlagDecode)) return;
+  if constexpr (!kind_decode(DT)) return;
   if (p.dec_token) p.dec_token[row] = token;
   if (p.dec_pos) p.dec_pos[row] = rs.dec_pos + 1;
   if (p.dec_count) p.dec_count[row] = rs.dec_count + 1u;
@@ -1154,13 +1182,14 @@ __device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, ui
 
 // A row that ends before the chain. A raw decode row leaves the caller's
 // candidates buffer as it was.
+template <int DT>
 __device__ __forceinline__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status,
                                                  const RowState& rs) {
   if (threadIdx.x == 0) {
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
     if (p.out_kept_count && !rs.raw) p.out_kept_count[row] = 0;
-    decode_advance(p, row, token, rs);
+    decode_advance<DT>(p, row, token, rs);
   }
 }
 
@@ -1218,6 +1247,7 @@ __device__ __forceinline__ uint32_t wave_compact(uint32_t* ids, float* pr, uint3
 // block barriers: parallel stages split the candidates over the lanes; the
 // reference's ordered sums run in every lane at once (seq_chain), so each lane
 // holds each result.
+template <int DT>
 __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32_t row, uint32_t n,
                            ChainBufs bf, const RowState& rs, const LibmTables& tab) {
   const uint32_t l = threadIdx.x;
@@ -1435,7 +1465,7 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
     if (p.out_kept_count && !rs.raw) p.out_kept_count[row] = len;
-    decode_advance(p, row, token, rs);
+    decode_advance<DT>(p, row, token, rs);
   }
   const uint32_t nk = rs.raw ? 0u : (uint32_t)min((int64_t)len, p.kept_ld);
   for (uint32_t i = l; i < nk; i += 64) {
@@ -1641,20 +1671,23 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   rs.rng = rin.rng;
   rs.history_len = rin.history_len;
   rs.raw = rin.raw;
-  const bool dec = (p.flags & kFlagDecode) != 0;
-  rs.dec_pos = dec && p.dec_pos ? p.dec_pos[row] : 0;
-  rs.dec_count = dec && p.dec_count ? p.dec_count[row] : 0u;
+  rs.dec_pos = 0;
+  rs.dec_count = 0;
+  if constexpr (kind_decode(DT)) {
+    if (p.dec_pos) rs.dec_pos = p.dec_pos[row];
+    if (p.dec_count) rs.dec_count = p.dec_count[row];
+  }
   store_libm_tables(tabv, s_tab);
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
 
 
   const uint32_t M = max(c.top_k, 256u);
   if (M > (uint32_t)kMaxM || (r.dry && min(r.hlen, r.dry_range) > (uint32_t)kDryMax)) {
-    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // sizes this build does not run on the device
+    write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // sizes this build does not run on the device
     return;
   }
   if (c.mirostat_mode != OXS_MIROSTAT_DISABLED && !p.mu) {
-    write_row_result(p, row, 0u, OXS_ROW_MISSING_STATE, rs);
+    write_row_result<DT>(p, row, 0u, OXS_ROW_MISSING_STATE, rs);
     return;
   }
   // DRY rows: their values, then the exact path (the stream kernel's
@@ -1757,7 +1790,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
 
   if (path == 0) {
     if (meff == 0) {  // every logit -inf or NaN (:267-270)
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
+      write_row_result<DT>(p, row, 0u, OXS_ROW_EMPTY, rs);
       return;
     }
     const uint32_t span_k = s_bstart[last] + s_bcount[last];  // keys in buckets 0 .. last
@@ -1789,7 +1822,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     } else {
       meff = min(M, N);
       if (meff == 0) {
-        write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
+        write_row_result<DT>(p, row, 0u, OXS_ROW_EMPTY, rs);
         return;
       }
       keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
@@ -1798,7 +1831,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   if (path == 2) {
     meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)s_keys, s_bcount, s_top, ts);
     if (meff == 0) {
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
+      write_row_result<DT>(p, row, 0u, OXS_ROW_EMPTY, rs);
       return;
     }
     bitonic_sort<false>(s_top, meff);
@@ -1816,7 +1849,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   bf.aux = (float*)(scratch + 2 * kChainLd);
   bf.aux64 = (uint64_t*)(scratch + 3 * kChainLd);
   bf.hit = s_hit;
-  wave_chain(p, c, row, meff, bf, rs, s_tab);
+  wave_chain<DT>(p, c, row, meff, bf, rs, s_tab);
 }
 
 // ---------------------------------------------------------------- host side
@@ -1876,7 +1909,7 @@ template <int DT, bool VEC, bool MASK>
 static hipError_t launch_slots(int slots, const Params& p, uint32_t grid, hipStream_t st) {
   switch (slots) {
     case 8:
-      if constexpr (DT == OXS_DTYPE_F32) return launch_stream<DT, 8, VEC, MASK>(p, grid, st);
+      if constexpr (kind_f32(DT)) return launch_stream<DT, 8, VEC, MASK>(p, grid, st);
       return hipErrorInvalidValue;  // bf16 chunks stop at 4 slots (8192 logits)
     case 4: return launch_stream<DT, 4, VEC, MASK>(p, grid, st);
     case 2: return launch_stream<DT, 2, VEC, MASK>(p, grid, st);
@@ -1884,15 +1917,33 @@ static hipError_t launch_slots(int slots, const Params& p, uint32_t grid, hipStr
   }
 }
 
-template <int DT>
+// KIND: the tail's kind; the stream kernel's is the same without the decode bit.
+template <int KIND>
 static hipError_t launch_all(int slots, bool vec, bool mask, const Params& p, uint32_t grid_a,
                              uint32_t grid_b, hipStream_t st) {
+  constexpr int SK = KIND & ~kKindDecode;
   hipError_t e;
-  if (vec) e = mask ? launch_slots<DT, true, true>(slots, p, grid_a, st) : launch_slots<DT, true, false>(slots, p, grid_a, st);
-  else e = mask ? launch_slots<DT, false, true>(slots, p, grid_a, st) : launch_slots<DT, false, false>(slots, p, grid_a, st);
+  if (vec) e = mask ? launch_slots<SK, true, true>(slots, p, grid_a, st) : launch_slots<SK, true, false>(slots, p, grid_a, st);
+  else e = mask ? launch_slots<SK, false, true>(slots, p, grid_a, st) : launch_slots<SK, false, false>(slots, p, grid_a, st);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((tail_kernel<DT>), dim3(grid_b), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((tail_kernel<KIND>), dim3(grid_b), dim3(kThreads), 0, st, p);
   return hipGetLastError();
+}
+
+static hipError_t launch_kind(int kind, int slots, bool vec, bool mask, const Params& p, uint32_t grid_a,
+                              uint32_t grid_b, hipStream_t st) {
+  constexpr int F = OXS_DTYPE_F32, H = OXS_DTYPE_BF16, S = kKindSoftcap, D = kKindDecode;
+  switch (kind) {
+    case F: return launch_all<F>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H: return launch_all<H>(slots, vec, mask, p, grid_a, grid_b, st);
+    case F | S: return launch_all<F | S>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H | S: return launch_all<H | S>(slots, vec, mask, p, grid_a, grid_b, st);
+    case F | D: return launch_all<F | D>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H | D: return launch_all<H | D>(slots, vec, mask, p, grid_a, grid_b, st);
+    case F | S | D: return launch_all<F | S | D>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H | S | D: return launch_all<H | S | D>(slots, vec, mask, p, grid_a, grid_b, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace oxs
@@ -2083,6 +2134,7 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
   p.kept_ld = (b->out_kept_ids || b->out_kept_probs) ? b->kept_ld : 0;
   p.logits_out = b->logits_out;
   p.logits_out_ld = b->logits_out_ld;
+  p.softcap = b->logit_softcap > 0.0f ? b->logit_softcap : 0.0f;  // NaN and <= 0: off (lib.rs:3244)
   p.S = g.S;
   p.CH = g.CH;
   p.cap_w = g.cap_w;
@@ -2112,9 +2164,8 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
   const uint32_t grid_a = b->batch * g.S;
   const uint32_t grid_b = b->batch;
   hipStream_t st = (hipStream_t)stream;
-  const hipError_t e = b->logits_dtype == OXS_DTYPE_F32
-                           ? launch_all<OXS_DTYPE_F32>(g.slots, vec, mask, p, grid_a, grid_b, st)
-                           : launch_all<OXS_DTYPE_BF16>(g.slots, vec, mask, p, grid_a, grid_b, st);
+  const int kind = b->logits_dtype | (p.softcap > 0.0f ? kKindSoftcap : 0) | (io ? kKindDecode : 0);
+  const hipError_t e = launch_kind(kind, g.slots, vec, mask, p, grid_a, grid_b, st);
   return e == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }
 

@@ -12,7 +12,7 @@ from pathlib import Path
 PKG_ROOT = Path(__file__).resolve().parent.parent  # oxide-tech-llm-engine_amd/
 LIB_PATH = PKG_ROOT / "lib" / "liboxide_sampler.so"
 
-OXS_ABI_VERSION = 2
+OXS_ABI_VERSION = 3
 
 OXS_OK = 0
 OXS_ERR_INVALID_ARGUMENT = -1
@@ -127,6 +127,7 @@ class OxsBatch(ctypes.Structure):
         ("kept_ld", ctypes.c_int64),
         ("logits_out", ctypes.c_void_p),
         ("logits_out_ld", ctypes.c_int64),
+        ("logit_softcap", ctypes.c_float),
     ]
 
 

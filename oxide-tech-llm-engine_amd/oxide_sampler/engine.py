@@ -207,14 +207,15 @@ class BatchSampler:
                mask=None, history=None, history_len=None, history_cap: Optional[int] = None,
                record: bool = False, uniforms=None, rng_state=None, mirostat_mu=None,
                kept_ld: int = 0, logits_out=None, stream=None, decode: Optional[OxsDecodeIo] = None,
-               out: Optional[dict] = None):
+               out: Optional[dict] = None, softcap: float = 0.0):
         """Samples every row of `logits` ([B, V] f32/bf16 CUDA tensor).
 
         `configs` is a uint8 CUDA tensor holding B (or 1 with shared_config)
         packed `oxs_sampling_config` records. Returns a dict of output tensors
         (tokens, status, kept_count and, with kept_ld > 0, kept_ids/kept_probs),
         the ones of `out` when given. With `decode` (an OxsDecodeIo) the call
-        is a decode step (oxs_decode_step).
+        is a decode step (oxs_decode_step). `softcap` > 0 applies the model's
+        final logit softcap as the logits are read.
         """
         t = self.torch
         dev = logits.device
@@ -268,6 +269,7 @@ class BatchSampler:
         if logits_out is not None:
             b.logits_out = logits_out.data_ptr()
             b.logits_out_ld = int(logits_out.stride(0))
+        b.logit_softcap = float(softcap)
         self.launch(b, stream, decode)
         return out
 

@@ -42,7 +42,8 @@ def run_oracle(w: Workload, kept_ld: int = 256, record: bool = True, use_rng: bo
         _abi, logits=np.ascontiguousarray(w.logits), dtype=w.dtype, configs_bytes=cfg, bias_ids=bias_ids,
         bias_values=bias_vals, ban_ids=ban_ids, mask=w.mask, history=history, history_len=hist_len,
         history_cap=history.shape[1], record=record, uniforms=None if use_rng else w.uniforms,
-        rng_state=rng, mu=mu, kept_ld=kept_ld, logits_out=lo, n_threads=n_threads)
+        rng_state=rng, mu=mu, kept_ld=kept_ld, logits_out=lo, n_threads=n_threads,
+        softcap=float(w.extra.get("softcap", 0.0)))
     return Result(out["tokens"], out["status"], out["kept_count"], out["kept_ids"][:, :kept_ld],
                   out["kept_probs"][:, :kept_ld], history, hist_len, mu, rng, lo)
 
@@ -90,7 +91,7 @@ def run_gpu(w: Workload, torch, kept_ld: int = 256, record: bool = True, use_rng
         ban_ids=torch.from_numpy(ban_ids.view(np.int32)).to(d) if ban_ids.size else None,
         mask=mask, history=hist, history_len=hlen, history_cap=w.history.shape[1], record=record,
         uniforms=None if use_rng else torch.from_numpy(w.uniforms).to(d), rng_state=rng,
-        mirostat_mu=mu, kept_ld=kept_ld, logits_out=lo)
+        mirostat_mu=mu, kept_ld=kept_ld, logits_out=lo, softcap=float(w.extra.get("softcap", 0.0)))
     torch.cuda.synchronize()
     return Result(
         out["tokens"].cpu().numpy().view(np.uint32), out["status"].cpu().numpy(),

@@ -1,5 +1,5 @@
 // Sweeps the device libm emulation (oxs_libm.h, compiled here as host C++)
-// against the host's glibc expf/logf/log2f/powf, bit for bit.
+// against the host's glibc expf/logf/log2f/powf/tanhf, bit for bit.
 //
 // usage: libm_sweep FUSED STRIDE
 //   FUSED  1 compares the fused-multiply-add form (what glibc's ifunc picks on
@@ -62,11 +62,23 @@ int run(uint64_t stride) {
     const float y2 = u2f((uint32_t)(b * 2654435761ull));
     tp.add((uint32_t)b, same(powf_t<FUSED>(x, y2), powf(x, y2)));
   }
+  // tanhf (one form: plain float steps): the stride sweep, plus every float
+  // in [-40, 40], the arguments l / cap of logit softcaps
+  Tally tt;
+  for (uint64_t b = 0; b <= 0xffffffffull; b += stride) {
+    const float x = u2f((uint32_t)b);
+    tt.add((uint32_t)b, same(tanhf_fdlibm(x), tanhf(x)));
+  }
+  for (uint32_t b = 0; b <= f2u(40.0f); b += 3) {
+    const float x = u2f(b);
+    tt.add(b, same(tanhf_fdlibm(x), tanhf(x)) && same(tanhf_fdlibm(-x), tanhf(-x)));
+  }
   printf("expf %llu %llu %08x\n", te.checked, te.bad, te.first);
+  printf("tanhf %llu %llu %08x\n", tt.checked, tt.bad, tt.first);
   printf("powf %llu %llu %08x\n", tp.checked, tp.bad, tp.first);
   printf("logf %llu %llu %08x\n", tl.checked, tl.bad, tl.first);
   printf("log2f %llu %llu %08x\n", t2.checked, t2.bad, t2.first);
-  return (te.bad | tl.bad | t2.bad | tp.bad) ? 1 : 0;
+  return (te.bad | tl.bad | t2.bad | tp.bad | tt.bad) ? 1 : 0;
 }
 
 }  // namespace

@@ -1,7 +1,7 @@
-"""The device's expf/logf/log2f/powf (oxs_libm.h) against the host glibc, bit for bit.
+"""The device's expf/logf/log2f/powf/tanhf (oxs_libm.h) against the host glibc, bit for bit.
 
 The GPU kernels reproduce the reference's f32::{exp, ln, log2}
-(sampler.rs:289, :424, :440, :451, :496, :502) and f32::powf (:409, DRY), which
+(sampler.rs:289, :424, :440, :451, :496, :502) and f32::powf (:409, DRY), and f32::tanh for the logit softcap, which
 lower to glibc on
 x86_64-linux-gnu. oxs_libm.h compiles as plain host C++ too, so this test
 builds tests/libm_sweep.cpp with g++ and compares every 197th float bit
@@ -40,7 +40,7 @@ def test_device_libm_matches_host_glibc(sweep_bin, fused):
         pass
     res = subprocess.run([str(sweep_bin), str(fused), "197"], capture_output=True, text=True, timeout=300)
     lines = dict((l.split()[0], l.split()[1:]) for l in res.stdout.strip().splitlines())
-    assert set(lines) == {"expf", "logf", "log2f", "powf"}, res.stdout + res.stderr
+    assert set(lines) == {"expf", "logf", "log2f", "powf", "tanhf"}, res.stdout + res.stderr
     for fn, (checked, bad, first) in lines.items():
         assert int(checked) > (500_000 if fn == "powf" else 10_000_000), f"{fn}: sweep too small"
         if fused == 1 or not _host_has_fma():
