@@ -228,13 +228,13 @@ typedef struct oxs_decode_io {
   uint32_t* current_token;    /* [B] set to the sampled token: the next step's input (:974) */
   int32_t* current_position;  /* [B] += 1 (:975) */
   uint32_t* generated_count;  /* [B] += 1 (:976) */
-  /* Host memory from oxs_host_alloc (megakernel_ops.cu:331-347's h_sampled_token):
-   * host_tokens[B] receives the tokens and, once every row's host token is
-   * visible, *host_seq receives the number of steps with host_seq set that
-   * this sampler has completed, so the host can poll it instead of
-   * synchronising the stream. */
-  uint32_t* host_tokens;
-  uint32_t* host_seq;
+  /* Host memory from oxs_host_alloc (megakernel_ops.cu:331-347's
+   * h_sampled_token and its step counter): host_tokens[b] receives
+   * (n << 32) | token in one 8-byte store, where n counts the decode steps on
+   * this sampler that passed host_tokens and included row b (the first one
+   * writes n = 1). The host polls each row's slot for its expected n instead
+   * of synchronising the stream. */
+  uint64_t* host_tokens;
 } oxs_decode_io;
 
 /*
@@ -248,7 +248,7 @@ typedef struct oxs_decode_io {
  *     exactly as in oxs_sample_batch (:971-972); a failing row gives token 0
  *     (unwrap_or(0), :973);
  *   - then io's arrays are advanced (:974-976) and the tokens handed to the
- *     host. Calls that overlap on one sampler race on its step counter.
+ *     host. Calls that overlap on one sampler race on its per-row step counts.
  * Same arguments and errors as oxs_sample_batch, plus `io`; asynchronous;
  * allocates nothing and issues only kernels, so it can be captured in a HIP
  * graph. newline_token_id is the config's (the loop passes 10, :972).

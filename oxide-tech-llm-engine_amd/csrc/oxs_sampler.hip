@@ -114,9 +114,8 @@ struct Params {
   uint32_t* dec_token;    // [B] next step's input token
   int32_t* dec_pos;       // [B] position
   uint32_t* dec_count;    // [B] generated count
-  uint32_t* host_tokens;  // [B] host memory
-  uint32_t* host_seq;     // host memory: completed steps
-  uint32_t* ticket;       // [0] rows finished in this launch (0 between launches), [1] steps published
+  uint64_t* host_tokens;  // [B] host memory: (row's step count << 32) | token
+  uint32_t* row_steps;    // [B] workspace: decode steps each row has handed to the host
 };
 
 // ---------------------------------------------------------------- keys
@@ -1146,37 +1145,29 @@ struct RowState {
   uint64_t rng;
   uint32_t history_len;
   bool raw;            // a raw decode row: no history, no candidates buffer
-  int32_t dec_pos;     // decode step: the row's position and generated count
-  uint32_t dec_count;
+  int32_t dec_pos;     // decode step: the row's position and generated count,
+  uint32_t dec_count;  // and the steps it has handed to the host
+  uint32_t dec_steps;
 };
 
 // The decode loop's bookkeeping once a row's token is known, by the thread
 // that wrote it (continuous_batching.rs:974-976; the device-side advance and
 // host hand-off of megakernel_ops.cu:331-347): the next step's input token,
-// position and generated count, the token in host memory and, from the row
-// that finishes last, the host's step counter, released after every row's
-// host token.
+// position and generated count, and the token in host memory. The host slot
+// is one 8-byte system-scope store of (the row's step count << 32 | token),
+// written through to host memory: the host polls each slot for its expected
+// count, so no row waits for another or for the store's acknowledgement.
 template <int DT>
 __device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, uint32_t token, const RowState& rs) {
   if constexpr (!kind_decode(DT)) return;
   if (p.dec_token) p.dec_token[row] = token;
   if (p.dec_pos) p.dec_pos[row] = rs.dec_pos + 1;
   if (p.dec_count) p.dec_count[row] = rs.dec_count + 1u;
-  // The host token is a system-scope store (written through to host memory);
-  // the ticket is a release at agent scope, so no row invalidates its L2. The
-  // row that takes the last ticket acquires every row's release, counts the
-  // step in device memory and publishes the count with one system-scope
-  // release (ticket[0]: rows done in this launch; ticket[1]: steps done).
-  if (p.host_tokens) __hip_atomic_store(p.host_tokens + row, token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  if (p.host_seq) {
-    const uint32_t done = __hip_atomic_fetch_add(p.ticket, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == p.B - 1u) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t n = __hip_atomic_load(p.ticket + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-      __hip_atomic_store(p.ticket + 1, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.host_seq, n, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
+  if (p.host_tokens) {
+    const uint32_t n = rs.dec_steps + 1u;
+    p.row_steps[row] = n;
+    __hip_atomic_store(p.host_tokens + row, ((uint64_t)n << 32) | token, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -1673,9 +1664,11 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   rs.raw = rin.raw;
   rs.dec_pos = 0;
   rs.dec_count = 0;
+  rs.dec_steps = 0;
   if constexpr (kind_decode(DT)) {
     if (p.dec_pos) rs.dec_pos = p.dec_pos[row];
     if (p.dec_count) rs.dec_count = p.dec_count[row];
+    if (p.host_tokens) rs.dec_steps = p.row_steps[row];
   }
   store_libm_tables(tabv, s_tab);
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
@@ -1959,7 +1952,7 @@ struct oxs_sampler {
   uint64_t* libm;
   uint64_t* dry_list;
   uint32_t* dry_count;
-  uint32_t* ticket;  // decode steps: rows finished in the running launch, steps published
+  uint32_t* row_steps;  // [max_batch] decode steps each row has handed to the host
   size_t bytes;
 };
 
@@ -2040,9 +2033,10 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
                   hipMalloc((void**)&s->libm, oxs::kLibmWords * sizeof(uint64_t)) == hipSuccess &&
                   hipMalloc((void**)&s->dry_list, B * oxs::kDryMax * sizeof(uint64_t)) == hipSuccess &&
                   hipMalloc((void**)&s->dry_count, B * sizeof(uint32_t)) == hipSuccess &&
-                  hipMalloc((void**)&s->ticket, 256) == hipSuccess && hipMemset(s->ticket, 0, 256) == hipSuccess;
+                  hipMalloc((void**)&s->row_steps, B * sizeof(uint32_t)) == hipSuccess &&
+                  hipMemset(s->row_steps, 0, B * sizeof(uint32_t)) == hipSuccess;
   s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t) +
-             B * (oxs::kDryMax * sizeof(uint64_t) + sizeof(uint32_t)) + 256;
+             B * (oxs::kDryMax * sizeof(uint64_t) + 2 * sizeof(uint32_t));
   if (ok) {  // the libm tables, as bit patterns, in the workspace
     uint64_t host[oxs::kLibmWords];
     ok = hipMemcpyFromSymbol(host, HIP_SYMBOL(oxs_libm::kExp2Tab), 32 * sizeof(uint64_t)) == hipSuccess &&
@@ -2067,7 +2061,7 @@ int oxs_sampler_destroy(oxs_sampler* s) {
   if (s->libm) (void)hipFree(s->libm);
   if (s->dry_list) (void)hipFree(s->dry_list);
   if (s->dry_count) (void)hipFree(s->dry_count);
-  if (s->ticket) (void)hipFree(s->ticket);
+  if (s->row_steps) (void)hipFree(s->row_steps);
   free(s);
   return OXS_OK;
 }
@@ -2152,8 +2146,7 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
     p.dec_pos = io->current_position;
     p.dec_count = io->generated_count;
     p.host_tokens = io->host_tokens;
-    p.host_seq = io->host_seq;
-    p.ticket = s->ticket;
+    p.row_steps = s->row_steps;
   }
   // Group rows by XCD when the batch divides evenly over the 8 XCDs.
   p.rpx = (b->batch % 8 == 0) ? b->batch / 8 : 0;

@@ -153,7 +153,6 @@ class OxsDecodeIo(ctypes.Structure):
         ("current_position", ctypes.c_void_p),
         ("generated_count", ctypes.c_void_p),
         ("host_tokens", ctypes.c_void_p),
-        ("host_seq", ctypes.c_void_p),
     ]
 
 

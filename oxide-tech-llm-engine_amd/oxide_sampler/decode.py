@@ -13,8 +13,9 @@ One `oxs_decode_step` launch per step then does every slot's work:
 - otherwise sample_token with newline id 10, giving 0 on error;
 - the advance of current_token, position and count.
 
-The tokens land directly in host-mapped memory, and the host polls a step
-counter instead of copying logits back and synchronising the stream. The
+Each row's token lands directly in host-mapped memory, tagged with the row's
+step count in the same 8-byte store. The host polls the tags instead of
+copying logits back and synchronising the stream. The
 per-token bookkeeping stays on the host, as in the reference (:986-1030):
 stop tokens, the DFA state walk, accepting states and max_tokens. It is a few
 comparisons per sequence.
@@ -42,8 +43,6 @@ STOP_TOKENS = frozenset((0, 2, 128_001, 128_008, 128_009, 151_643, 151_645))
 NEWLINE_TOKEN_ID = 10
 
 _CFG_BYTES = ctypes.sizeof(_abi.OxsSamplingConfig)
-_SEQ_OFFSET = 0    # host block: the step counter ...
-_TOK_OFFSET = 64   # ... then the tokens
 
 
 @dataclass
@@ -126,13 +125,13 @@ class DecodeLoop:
         self.generated_count = t.zeros(S, dtype=t.int32, device=dev)
         self.out = {k: t.zeros(S, dtype=t.int32, device=dev) for k in ("tokens", "status", "kept_count")}
         host = ctypes.c_void_p()
-        check(self.lib.oxs_host_alloc(_TOK_OFFSET + 4 * S, ctypes.byref(host)), "oxs_host_alloc")
+        check(self.lib.oxs_host_alloc(8 * S, ctypes.byref(host)), "oxs_host_alloc")
         self._host = host.value
-        self._seq_word = ctypes.c_uint32.from_address(self._host + _SEQ_OFFSET)
-        self._host_tokens = (ctypes.c_uint32 * S).from_address(self._host + _TOK_OFFSET)
+        # slot b: (steps row b has completed << 32) | its last token
+        self._slots = np.frombuffer((ctypes.c_uint64 * S).from_address(self._host), dtype=np.uint64)
         self.io = OxsDecodeIo(self.current_token.data_ptr(), self.current_position.data_ptr(),
-                              self.generated_count.data_ptr(), self._host + _TOK_OFFSET, self._host + _SEQ_OFFSET)
-        self.launched = 0  # steps launched; the device counts completed ones in the host block
+                              self.generated_count.data_ptr(), self._host)
+        self.launched = 0  # steps launched; every step covers every slot
         self.active: Dict[int, Sequence] = {}
         self._graph = None
 
@@ -216,18 +215,22 @@ class DecodeLoop:
         return self.launched
 
     def completed(self) -> int:
-        """Steps the device has finished (the host block's counter)."""
-        return int(self._seq_word.value)
+        """Steps the device has finished for every slot (the smallest tag)."""
+        return int((self._slots.copy() >> np.uint64(32)).min())
 
     def wait(self, step: Optional[int] = None, timeout: float = 30.0) -> np.ndarray:
-        """Polls the host block until step `step` (default: the last launched)
-        is done, then returns the tokens of every slot; no stream sync."""
+        """Polls the host slots until every row carries step `step` (default:
+        the last launched), then returns the tokens of every slot; no stream
+        sync. Each slot is one 8-byte store, so its token belongs to its tag."""
         want = (self.launched if step is None else int(step)) & 0xFFFFFFFF
         deadline = time.monotonic() + timeout
-        while ((self._seq_word.value - want) & 0xFFFFFFFF) >= 0x80000000:
+        while True:
+            snap = self._slots.copy()
+            tags = (snap >> np.uint64(32)).astype(np.int64)
+            if np.all(((tags - want) & 0xFFFFFFFF) < 0x80000000):
+                return (snap & np.uint64(0xFFFFFFFF)).astype(np.uint32)
             if time.monotonic() > deadline:
                 raise TimeoutError(f"decode step {want} not finished after {timeout} s")
-        return np.ctypeslib.as_array(self._host_tokens).copy()
 
     def step(self, logits=None, mask=None) -> Dict[int, TokenEvent]:
         """One decode step: launches (or replays the captured step when
