@@ -153,11 +153,11 @@ typedef struct oxs_batch {
   float* out_kept_probs;    /* optional [B][kept_ld] */
   int64_t kept_ld;
 
-  /* Optional [B][logits_out_ld] f32: receives each row's logits after bans,
-   * biases, newline and window penalties and temperature, i.e. what the
-   * reference leaves in its `logits: &mut [f32]` argument (sampler.rs:184-254;
-   * checked by academic_samplers_test.rs:75), with masked ids at -inf. Must not
-   * overlap `logits`. */
+  /* Optional [B][logits_out_ld] f32: receives each row's logits after the
+   * softcap (if any), bans, biases, newline, DRY and window penalties and
+   * temperature, i.e. what the reference leaves in its `logits: &mut [f32]`
+   * argument (sampler.rs:184-254; checked by academic_samplers_test.rs:75),
+   * with masked ids at -inf. Must not overlap `logits`. */
   float* logits_out;
   int64_t logits_out_ld;
 
