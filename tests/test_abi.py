@@ -90,3 +90,42 @@ def test_create_rejects_bad_arguments_without_a_device(lib):
     assert lib.oxs_sampler_create(ctypes.byref(h), ctypes.byref(lim), 0) == _abi.OXS_ERR_INVALID_ARGUMENT
     assert lib.oxs_sample_batch(None, None, None) == _abi.OXS_ERR_INVALID_ARGUMENT
     assert lib.oxs_sampler_destroy(None) in (_abi.OXS_OK, _abi.OXS_ERR_INVALID_ARGUMENT)
+
+
+_STRUCTS = ("oxs_sampling_config", "oxs_limits", "oxs_batch", "oxs_decode_io", "oxs_dfa", "oxs_token_bytes")
+
+
+def _c_layouts(tmp_path):
+    """sizeof and every field's offset of the header's structs, from a C compiler."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    fields = {}
+    for name in _STRUCTS:
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S).group(1)
+        fields[name] = re.findall(r"(\w+)\s*;", body)
+    lines = ["#include <stddef.h>", "#include <stdio.h>", f'#include "{HEADER}"', "int main(void) {"]
+    for name, fs in fields.items():
+        lines.append(f'  printf("{name} sizeof %zu\\n", sizeof({name}));')
+        for f in fs:
+            lines.append(f'  printf("{name} {f} %zu\\n", offsetof({name}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    out = {}
+    for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        s, f, v = l.split()
+        out[(s, f)] = int(v)
+    return fields, out
+
+
+def test_ctypes_structs_match_the_header_layout(tmp_path):
+    # every struct the Python binding passes through the ABI, field by field
+    py = {"oxs_sampling_config": _abi.OxsSamplingConfig, "oxs_limits": _abi.OxsLimits, "oxs_batch": _abi.OxsBatch,
+          "oxs_decode_io": _abi.OxsDecodeIo, "oxs_dfa": _abi.OxsDfa, "oxs_token_bytes": _abi.OxsTokenBytes}
+    fields, c = _c_layouts(tmp_path)
+    for name, cls in py.items():
+        assert [f for f, _ in cls._fields_] == fields[name], name
+        assert ctypes.sizeof(cls) == c[(name, "sizeof")], name
+        for f in fields[name]:
+            assert getattr(cls, f).offset == c[(name, f)], (name, f)

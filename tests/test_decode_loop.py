@@ -330,3 +330,62 @@ def test_gpu_decode_loop_events_match_reference_loop(torch_gpu):
         if not loop.active:
             break
     loop.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,softcap", [("bf16", 0.0), ("f32", 20.0), ("bf16", 3.0)])
+def test_gpu_decode_step_bf16_softcap_mask(torch_gpu, dtype, softcap):
+    # the decode step's kernel kinds with bf16 logits, the softcap and a grammar mask
+    from oxide_sampler import BatchSampler
+    from oxide_sampler import workloads as wl
+    from oxide_sampler._abi import OxsDecodeIo
+    t = torch_gpu
+    B, V, cap = 24, 20001, 64
+    cfgs = decode_configs()
+    cfg_bytes = configs_to_array(cfgs, 10)[0]
+    history, hlen, mu, rng_state, dec = decode_state(B, cap, 21)
+    x = decode_logits(B, V, 1, history, hlen)
+    rng = np.random.default_rng(4)
+    bits = rng.random((B, V)) < 0.5
+    bits[:, :64] = True
+    mask = wl.pack_mask(bits, V)
+    if dtype == "bf16":
+        logits = wl.f32_to_bf16_bits(x)
+        d_logits = t.from_numpy(logits.view(np.int16).copy()).to("cuda").view(t.bfloat16)
+    else:
+        logits = x
+        d_logits = _to_dev(t, x)
+    d_hist, d_hlen, d_mu, d_rng = (_to_dev(t, a) for a in (history, hlen, mu, rng_state))
+    d_dec = {k: _to_dev(t, v) for k, v in dec.items()}
+    lib = _abi.load_library()
+    host = ctypes.c_void_p()
+    _abi.check(lib.oxs_host_alloc(8 * B, ctypes.byref(host)), "oxs_host_alloc")
+    try:
+        io = OxsDecodeIo(d_dec["current_token"].data_ptr(), d_dec["current_position"].data_ptr(),
+                         d_dec["generated_count"].data_ptr(), host.value)
+        s = BatchSampler(B, V, 256)
+        print(f"\n[case] decode step {dtype} softcap={softcap} masked", flush=True)
+        out = s.sample(d_logits, _to_dev(t, cfg_bytes), mask=_to_dev(t, mask), history=d_hist, history_len=d_hlen,
+                       history_cap=cap, record=True, rng_state=d_rng, mirostat_mu=d_mu, decode=io, softcap=softcap)
+        t.cuda.synchronize()
+        ref = oracle.sample_batch_host(
+            _abi, logits=logits, dtype=dtype, configs_bytes=cfg_bytes, bias_ids=None, bias_values=None,
+            ban_ids=None, mask=mask, history=history, history_len=hlen, history_cap=cap, record=True, uniforms=None,
+            rng_state=rng_state, mu=mu, kept_ld=1, decode=dec, softcap=softcap)
+        np.testing.assert_array_equal(_u32(out["tokens"]), ref["tokens"])
+        np.testing.assert_array_equal(out["status"].cpu().numpy(), ref["status"])
+        np.testing.assert_array_equal(_u32(d_hlen), hlen)
+        np.testing.assert_array_equal(_u32(d_hist), history)
+        np.testing.assert_array_equal(d_mu.cpu().numpy().view(np.uint32), mu.view(np.uint32))
+        np.testing.assert_array_equal(d_rng.cpu().numpy().view(np.uint64), rng_state)
+        for k in dec:
+            np.testing.assert_array_equal(d_dec[k].cpu().numpy().view(dec[k].dtype), dec[k])
+        slots = np.frombuffer((ctypes.c_uint64 * B).from_address(host.value), dtype=np.uint64).copy()
+        np.testing.assert_array_equal((slots & np.uint64(0xFFFFFFFF)).astype(np.uint32), ref["tokens"])
+        for b in range(B):  # every token allowed by the mask (or 0 for an empty row)
+            tok = int(ref["tokens"][b])
+            assert bits[b, tok] or ref["status"][b] == _abi.OXS_ROW_EMPTY
+        s.close()
+    finally:
+        t.cuda.synchronize()
+        lib.oxs_host_free(host)
