@@ -483,17 +483,6 @@ __device__ __forceinline__ uint32_t hash_lookup(const uint32_t* hkeys, const uin
 
 constexpr uint32_t kMinValidOrd = 0x00800000u;  // f2ord(-FLT_MAX): every candidate key is >= this
 
-// The (row, chunk) of a stream block. With rpx > 0 the hardware's round-robin
-// placement of blocks on the 8 XCDs (block i on XCD i % 8) gives XCD x the
-// chunks of rows [x * rpx, (x + 1) * rpx), so that a row's stream blocks and
-// its tail block share one L2.
-__device__ __forceinline__ void unit_of(const Params& p, uint32_t* row, uint32_t* chunk) {
-  const uint32_t k = p.rpx ? grouped_index(blockIdx.x, p.rpx * p.S) : blockIdx.x;
-  *row = k / p.S;
-  *chunk = k - *row * p.S;
-}
-
-
 // One unit after its logits arrived. The dense stages (grammar mask, end of
 // vocabulary) are applied in registers and the values are staged in LDS,
 // indexed by chunk offset. When the row has sparse-stage ids (history window,
@@ -685,8 +674,12 @@ __device__ __forceinline__ void build_marks(const Params& p, const RowXf& r, uin
 // second half. The marks are built when the window ids arrive, which waits
 // for the first half only (vector loads complete in issue order), while the
 // second half is still in flight.
+// The arguments before the Params copy are what the first loads need; they
+// arrive in SGPRs at wave launch (kernel-argument preloading), so those loads
+// issue without waiting for a kernel-argument fetch.
 template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
-__global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
+__global__ __launch_bounds__(kThreads) void stream_kernel(const void* __restrict__ logits, int64_t ld, uint32_t S,
+                                                          uint32_t rpx, uint32_t B, uint32_t V, const Params p) {
   constexpr int EPL = kind_f32(DT) ? 4 : 8;  // logits per 16-byte load
   constexpr int TILE = kThreads * EPL;
   constexpr int CH = SLOTS * TILE;
@@ -702,20 +695,24 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const Params p) {
   __shared__ uint32_t s_full;
 
   const uint32_t tid = threadIdx.x;
-  uint32_t row, chunk;
-  unit_of(p, &row, &chunk);
-  if (row >= p.B) return;
+  // the block's (row, chunk). With rpx > 0 the hardware's round-robin
+  // placement of blocks on the 8 XCDs (block i on XCD i % 8) gives XCD x the
+  // chunks of rows [x * rpx, (x + 1) * rpx), so that a row's stream blocks and
+  // its tail block share one L2.
+  const uint32_t k = rpx ? grouped_index(blockIdx.x, rpx * S) : blockIdx.x;
+  const uint32_t row = k / S, chunk = k - row * S;
+  if (row >= B) return;
   const uint32_t c0 = chunk * CH;
-  const uint32_t c1 = min(c0 + (uint32_t)CH, p.V);
+  const uint32_t c1 = min(c0 + (uint32_t)CH, V);
 
   uint32_t raw[SLOTS][EPL];
-  const char* rowp = (const char*)p.logits + (size_t)row * (size_t)p.ld * ESZ;
+  const char* rowp = (const char*)logits + (size_t)row * (size_t)ld * ESZ;
   auto load_slot = [&](int s) {
     const uint32_t base = c0 + s * TILE + tid * EPL;
     if constexpr (VEC) {
       // V is a multiple of EPL here: past-the-end groups re-read the row's
       // last group (in bounds) and their values are dropped later.
-      const uint32_t at = base < c1 ? base : p.V - EPL;
+      const uint32_t at = base < c1 ? base : V - EPL;
       const u32x4 q = __builtin_nontemporal_load((const u32x4*)(rowp + (size_t)at * ESZ));
       if constexpr (kind_f32(DT)) {
         raw[s][0] = q.x; raw[s][1] = q.y; raw[s][2] = q.z; raw[s][3] = q.w;
@@ -1606,7 +1603,13 @@ __device__ void keys_to_chain(const uint64_t* keys, uint32_t n, uint32_t* ids, f
 }
 
 template <int DT>
-__global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
+// Leading arguments: what the first loads need, preloaded into SGPRs as in
+// stream_kernel.
+__global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restrict__ wave_theta,
+                                                        const uint64_t* __restrict__ lists,
+                                                        const uint32_t* __restrict__ wave_count,
+                                                        const uint64_t* __restrict__ libm, uint32_t S, uint32_t cap_w,
+                                                        uint32_t cap_shift, uint32_t rpx, uint32_t B, const Params p) {
   __shared__ __align__(16) uint64_t s_keys[kTailArea];  // bucket scatter / sort / exact-path table / chain scratch
   static_assert(kTailArea >= kUnionMax && kTailArea * 2 >= kMaxChunk, "tail LDS area");
   __shared__ __align__(16) uint64_t s_top[kMaxM];       // sorted top-M keys (sort and exact paths)
@@ -1621,8 +1624,8 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
                 "chain scratch fits the key area");
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t row = p.rpx ? grouped_index(blockIdx.x, p.rpx) : blockIdx.x;
-  if (row >= p.B) return;
+  const uint32_t row = rpx ? grouped_index(blockIdx.x, rpx) : blockIdx.x;
+  if (row >= B) return;
 
   // 1. the row's reads, issued before anything waits: the wavefront
   // thresholds, the candidate slots (two per 16-byte load) with the count of
@@ -1630,18 +1633,18 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   // addresses need nothing from memory), then the row's record (config,
   // history length, uniform, mu, rng) through the scalar cache, whose wait
   // does not cover the vector loads
-  const uint32_t W = p.S * kWavesPerBlock;
-  const uint32_t span = W * p.cap_w;  // even: cap_w >= 8
+  const uint32_t W = S * kWavesPerBlock;
+  const uint32_t span = W * cap_w;  // even: cap_w >= 8
   uint64_t wr[kRecPer];  // every wavefront reads all W records (lane + 64 q; clamped repeats change no maximum)
 #pragma unroll
   for (int q = 0; q < kRecPer; ++q) {
     const uint32_t w = lane + 64u * q;
-    wr[q] = p.wave_theta[(size_t)row * W + (w < W ? w : W - 1u)];
+    wr[q] = wave_theta[(size_t)row * W + (w < W ? w : W - 1u)];
   }
   uint64_t lk[kPer];
   uint32_t lc[kPer / 2];
-  const ulonglong2* lrow = (const ulonglong2*)(p.lists + (size_t)row * span);
-  const uint32_t* wcrow = p.wave_count + (size_t)row * W;
+  const ulonglong2* lrow = (const ulonglong2*)(lists + (size_t)row * span);
+  const uint32_t* wcrow = wave_count + (size_t)row * W;
 #pragma unroll
   for (int q = 0; q < kPer / 2; ++q) {  // unconditional loads (clamped index): no branches between them
     const uint32_t pair = tid + q * kThreads;
@@ -1649,9 +1652,9 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
     const ulonglong2 k2 = lrow[at];
     lk[2 * q] = k2.x;
     lk[2 * q + 1] = k2.y;
-    lc[q] = wcrow[(2u * at) >> p.cap_shift];
+    lc[q] = wcrow[(2u * at) >> cap_shift];
   }
-  const LibmEntries tabv = fetch_libm_tables(p.libm);
+  const LibmEntries tabv = fetch_libm_tables(libm);
   __builtin_amdgcn_sched_barrier(0);  // every vector read above is issued before anything waits
   const RowIn rin = load_row_in(p, row);
   const oxs_sampling_config c = rin.cfg;
@@ -1698,7 +1701,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const Params p) {
   for (int q = 0; q < kPer; ++q) {
     const uint32_t slot = 2u * (tid + (q / 2) * kThreads) + (q & 1);
     const uint64_t k = lk[q];
-    if (slot < span && (slot & (p.cap_w - 1u)) < lc[q / 2] && k != 0ull) {
+    if (slot < span && (slot & (cap_w - 1u)) < lc[q / 2] && k != 0ull) {
       valid |= 1u << q;
       kmn = k < kmn ? k : kmn;
     }
@@ -1892,9 +1895,11 @@ static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
 template <int DT, int SLOTS, bool VEC, bool MASK>
 static hipError_t launch_stream(const Params& p, uint32_t grid, hipStream_t st) {
   if (p.logits_out)
-    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, true>), dim3(grid), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, true>), dim3(grid), dim3(kThreads), 0, st, p.logits, p.ld,
+                       p.S, p.rpx, p.B, p.V, p);
   else
-    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, false>), dim3(grid), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, false>), dim3(grid), dim3(kThreads), 0, st, p.logits,
+                       p.ld, p.S, p.rpx, p.B, p.V, p);
   return hipGetLastError();
 }
 
@@ -1919,7 +1924,9 @@ static hipError_t launch_all(int slots, bool vec, bool mask, const Params& p, ui
   if (vec) e = mask ? launch_slots<SK, true, true>(slots, p, grid_a, st) : launch_slots<SK, true, false>(slots, p, grid_a, st);
   else e = mask ? launch_slots<SK, false, true>(slots, p, grid_a, st) : launch_slots<SK, false, false>(slots, p, grid_a, st);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((tail_kernel<KIND>), dim3(grid_b), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((tail_kernel<KIND>), dim3(grid_b), dim3(kThreads), 0, st, (const uint64_t*)p.wave_theta,
+                     (const uint64_t*)p.lists, (const uint32_t*)p.wave_count, p.libm, p.S, p.cap_w, p.cap_shift, p.rpx,
+                     p.B, p);
   return hipGetLastError();
 }
 
