@@ -5,10 +5,10 @@
 // crates/oxide-server/src/grammar_engine.rs:42-65) and writes the packed
 // allowed-token bitmask that oxs_sample_batch reads (oxs_batch.allowed_mask).
 //
-// One thread per token: its first kMaxBytes bytes are read once into registers
-// and walked for every row of the block's row group, four rows at a time so
-// that four independent table reads are in flight per step. The table sits in
-// LDS when it fits. A walk is a chain of dependent table reads, so the table
+// One thread per token: its bytes are read kMaxBytes at a time into registers,
+// once, and each piece is walked from every row of the block's row group, whose
+// states stay in registers, four rows interleaved so that four independent
+// table reads are in flight per step. The table sits in LDS when it fits. A walk is a chain of dependent table reads, so the table
 // lookups bound this kernel, not HBM (the token bytes and offsets are read once
 // per row group). A wavefront's 64 consecutive tokens give two mask words per
 // row from one ballot.
@@ -28,10 +28,10 @@ constexpr int kThreads = 256;
 constexpr int kTokPerThread = 4;      // tokens per thread (amortises the table's load into LDS)
 constexpr int kRowsPerBlock = 16;     // rows walked per block
 constexpr int kRowIlp = 4;            // rows walked together
-constexpr int kMaxBytes = 16;         // bytes held in registers; longer tokens read the rest from memory
+constexpr int kMaxBytes = 16;         // token bytes read and walked per piece
 constexpr uint32_t kLdsStates = 48;   // tables of up to 48 states (48 KB) are copied into LDS
 constexpr uint32_t kErr = OXS_DFA_ERROR_STATE;
-static_assert(kRowsPerBlock % kRowIlp == 0, "row groups are walked kRowIlp at a time");
+static_assert(kRowsPerBlock % kRowIlp == 0, "rows are walked kRowIlp at a time");
 
 struct Params {
   const uint32_t* trans;
@@ -72,6 +72,9 @@ __global__ __launch_bounds__(kThreads) void dfa_mask_kernel(const Params p) {
   const uint32_t r0 = blockIdx.y * kRowsPerBlock;
   const uint32_t nr = min((uint32_t)kRowsPerBlock, p.B - r0);
   const uint32_t words = (p.V + 31u) / 32u;
+  uint32_t st0[kRowsPerBlock];  // the row group's start states
+#pragma unroll
+  for (int q = 0; q < kRowsPerBlock; ++q) st0[q] = p.states[r0 + ((uint32_t)q < nr ? q : 0u)];
   for (int k = 0; k < kTokPerThread; ++k) {
     // consecutive tokens per wavefront, the wavefront's first one 64-aligned
     const uint32_t t = (blockIdx.x * kTokPerThread + k) * kThreads + tid;
@@ -83,39 +86,44 @@ __global__ __launch_bounds__(kThreads) void dfa_mask_kernel(const Params p) {
       if (e >= b0 && e <= p.num_bytes) len = e - b0;
       else in = false;  // a range outside the byte array: not allowed, nothing read
     }
-    uint32_t by[kMaxBytes];
+    uint32_t s[kRowsPerBlock];
+    bool ok[kRowsPerBlock];
 #pragma unroll
-    for (int j = 0; j < kMaxBytes; ++j) by[j] = (uint32_t)j < len ? p.bytes[b0 + j] : 0u;
+    for (int q = 0; q < kRowsPerBlock; ++q) {
+      s[q] = st0[q];
+      ok[q] = in && (uint32_t)q < nr;
+    }
+    // the token's bytes kMaxBytes at a time, each piece read once and walked
+    // from every row's state (kRowIlp rows interleaved); a lane stops when no
+    // row can still allow its token
+    for (uint32_t j0 = 0; j0 < len; j0 += kMaxBytes) {
+      uint32_t by[kMaxBytes];
+#pragma unroll
+      for (int j = 0; j < kMaxBytes; ++j) by[j] = j0 + j < len ? p.bytes[b0 + j0 + j] : 0u;
+      const uint32_t n = min(len - j0, (uint32_t)kMaxBytes);
+#pragma unroll
+      for (int q0 = 0; q0 < kRowsPerBlock; q0 += kRowIlp) {
+#pragma unroll
+        for (int j = 0; j < kMaxBytes; ++j) {
+          if ((uint32_t)j < n) {
+#pragma unroll
+            for (int q = q0; q < q0 + kRowIlp; ++q) step(T, ns, by[j], s[q], ok[q]);
+          }
+        }
+      }
+      bool any = false;
+#pragma unroll
+      for (int q = 0; q < kRowsPerBlock; ++q) any |= ok[q];
+      if (!any) break;
+    }
     const uint32_t wbase = (t - lane) / 32u;  // the wavefront's first mask word
-    for (uint32_t r = 0; r < nr; r += kRowIlp) {
-      uint32_t s[kRowIlp];
-      bool ok[kRowIlp];
 #pragma unroll
-      for (int q = 0; q < kRowIlp; ++q) {
-        const bool live = r + q < nr;
-        s[q] = p.states[r0 + (live ? r + q : 0u)];
-        ok[q] = in && live;
-      }
-#pragma unroll
-      for (int j = 0; j < kMaxBytes; ++j) {
-        if ((uint32_t)j < len) {
-#pragma unroll
-          for (int q = 0; q < kRowIlp; ++q) step(T, ns, by[j], s[q], ok[q]);
-        }
-      }
-      for (uint32_t j = kMaxBytes; j < len; ++j) {  // tokens longer than kMaxBytes
-        const uint32_t b = p.bytes[b0 + j];
-#pragma unroll
-        for (int q = 0; q < kRowIlp; ++q) step(T, ns, b, s[q], ok[q]);
-      }
-#pragma unroll
-      for (int q = 0; q < kRowIlp; ++q) {
-        const uint64_t m = __ballot(ok[q]);
-        if (r + q < nr) {
-          uint32_t* row = p.mask + (size_t)(r0 + r + q) * p.mask_ld;
-          if (lane == 0 && wbase < words) row[wbase] = (uint32_t)m;
-          if (lane == 32 && wbase + 1 < words) row[wbase + 1] = (uint32_t)(m >> 32);
-        }
+    for (int q = 0; q < kRowsPerBlock; ++q) {
+      const uint64_t m = __ballot(ok[q]);
+      if ((uint32_t)q < nr) {
+        uint32_t* row = p.mask + (size_t)(r0 + q) * p.mask_ld;
+        if (lane == 0 && wbase < words) row[wbase] = (uint32_t)m;
+        if (lane == 32 && wbase + 1 < words) row[wbase + 1] = (uint32_t)(m >> 32);
       }
     }
   }
