@@ -129,6 +129,112 @@ __global__ __launch_bounds__(kThreads) void dfa_mask_kernel(const Params p) {
   }
 }
 
+// Tables of at most 64 states: each token is walked once from every start
+// state at the same time (independent lookups), leaving a 64-bit word whose
+// bit s says whether the token walks from state s; each row's mask bit is then
+// one test of its own state's bit. That is num_states x length lookups per
+// token instead of rows x length. A state outside the table allows only tokens
+// with no bytes. A block covers kStTok * 256 tokens and kStRows rows; the mask
+// words of kStBatch rows at a time are gathered in LDS from the wavefronts'
+// ballots and written as one contiguous run per row.
+constexpr uint32_t kSetStates = 64;
+constexpr int kStTok = 2;     // tokens per thread
+constexpr int kStRows = 32;   // rows per block
+constexpr int kStBatch = 8;   // rows staged in LDS per round
+constexpr int kStWords = kStTok * kThreads / 32;  // mask words per row and block
+template <int NS, bool LDS>  // NS: a bound on num_states (8, 16 or 64)
+__global__ __launch_bounds__(kThreads) void dfa_mask_states_kernel(const Params p) {
+  extern __shared__ __align__(16) uint32_t s_trans[];  // [num_states * 256] with LDS
+  __shared__ uint32_t s_words[kStBatch][kStWords];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (LDS) {
+    const uint32_t n4 = p.num_states * 64u;
+    for (uint32_t i = tid; i < n4; i += kThreads) ((uint4*)s_trans)[i] = ((const uint4*)p.trans)[i];
+    __syncthreads();
+  }
+  const uint32_t* T = LDS ? s_trans : p.trans;
+  const uint32_t ns = p.num_states;  // <= NS
+  const uint32_t words = (p.V + 31u) / 32u;
+  const uint32_t tbase = blockIdx.x * (kStTok * kThreads);
+  const uint32_t r0 = blockIdx.y * kStRows;
+  const uint32_t nr = min((uint32_t)kStRows, p.B - r0);
+  const uint32_t my_state = p.states[r0 + (lane < nr ? lane : 0u)];  // lane q holds row r0 + q's state
+  uint64_t alive[kStTok];
+  bool empty[kStTok];
+#pragma unroll
+  for (int k = 0; k < kStTok; ++k) {
+    const uint32_t t = tbase + k * kThreads + tid;
+    bool in = t < p.V;
+    uint32_t b0 = 0, len = 0;
+    if (in) {
+      b0 = p.offsets[t];
+      const uint32_t e = p.offsets[t + 1];
+      if (e >= b0 && e <= p.num_bytes) len = e - b0;
+      else in = false;  // a range outside the byte array: not allowed, nothing read
+    }
+    uint32_t cur[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) cur[s] = (uint32_t)s;
+    uint64_t a = ns >= 64u ? ~0ull : ((1ull << ns) - 1ull);
+    if (!in) a = 0;
+    // the bytes kMaxBytes at a time, all loads of a piece issued together
+    for (uint32_t j0 = 0; j0 < len && a; j0 += kMaxBytes) {
+      uint32_t by[kMaxBytes];
+#pragma unroll
+      for (int j = 0; j < kMaxBytes; ++j) by[j] = j0 + j < len ? p.bytes[b0 + j0 + j] : 0u;
+      const uint32_t n = min(len - j0, (uint32_t)kMaxBytes);
+#pragma unroll
+      for (int j = 0; j < kMaxBytes; ++j) {
+        if ((uint32_t)j < n) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            if ((a >> s) & 1ull) {  // (DfaSchemaGrammar::transition, dfa.rs:110-126)
+              const uint32_t c = cur[s];
+              const uint32_t nxt = c < ns ? T[c * 256u + by[j]] : kErr;
+              if (nxt == kErr) a &= ~(1ull << s);
+              cur[s] = nxt;
+            }
+          }
+        }
+      }
+    }
+    alive[k] = a;
+    empty[k] = in && len == 0;  // allowed from every state, even outside the table
+  }
+  static_assert(kStRows <= 64, "one row state per lane");
+  for (uint32_t rb = 0; rb < nr; rb += kStBatch) {
+#pragma unroll
+    for (int q = 0; q < kStBatch; ++q) {
+      if (rb + q < nr) {
+        const uint32_t st = (uint32_t)__builtin_amdgcn_readlane((int)my_state, (int)(rb + q));
+#pragma unroll
+        for (int k = 0; k < kStTok; ++k) {
+          const bool ok = st < ns ? ((alive[k] >> st) & 1ull) != 0 : empty[k];
+          const uint64_t m = __ballot(ok);
+          const uint32_t w = (k * kThreads + 64u * wave) / 32u;  // block-local word of this ballot
+          if (lane == 0) {
+            s_words[q][w] = (uint32_t)m;
+            s_words[q][w + 1] = (uint32_t)(m >> 32);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < (uint32_t)(kStBatch * kStWords)) {
+      const uint32_t q = tid / kStWords, w = tid % kStWords;
+      const uint32_t gw = blockIdx.x * kStWords + w;
+      if (rb + q < nr && gw < words) p.mask[(size_t)(r0 + rb + q) * p.mask_ld + gw] = s_words[q][w];
+    }
+    __syncthreads();
+  }
+}
+
+template <int NS>
+static void launch_states(const Params& p, dim3 grid, bool lds, size_t lds_bytes, hipStream_t st) {
+  if (lds) hipLaunchKernelGGL((dfa_mask_states_kernel<NS, true>), grid, dim3(kThreads), lds_bytes, st, p);
+  else hipLaunchKernelGGL((dfa_mask_states_kernel<NS, false>), grid, dim3(kThreads), 0, st, p);
+}
+
 // Row b of the output is row min(states[b], num_states) of the per-state
 // masks (row num_states holds the masks of every state outside the table).
 constexpr int kGatherWords = 4 * kThreads;  // words per gather block
@@ -159,7 +265,8 @@ extern "C" int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, c
     return OXS_ERR_INVALID_ARGUMENT;
   if (mask_ld < (int64_t)((tokens->vocab + 31u) / 32u)) return OXS_ERR_INVALID_ARGUMENT;
   // token indices stay below 2^31 and row groups within the grid's y extent
-  if (tokens->vocab > (1u << 31) || batch > 65535u * kRowsPerBlock) return OXS_ERR_INVALID_ARGUMENT;
+  if (tokens->vocab > (1u << 31) || batch > 65535u * (uint32_t)min(kRowsPerBlock, kStRows))
+    return OXS_ERR_INVALID_ARGUMENT;
   Params p;
   p.trans = dfa->transitions;
   p.num_states = dfa->num_states;
@@ -171,14 +278,21 @@ extern "C" int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, c
   p.B = batch;
   p.mask = mask;
   p.mask_ld = mask_ld;
-  const uint32_t per_block = (uint32_t)(kThreads * kTokPerThread);
-  const dim3 grid((p.V + per_block - 1) / per_block, (batch + kRowsPerBlock - 1) / kRowsPerBlock);
   hipStream_t st = (hipStream_t)stream;
   // the table is copied into LDS in 16-byte pieces: small and 16-byte aligned tables only
-  if (p.num_states <= kLdsStates && ((uintptr_t)p.trans & 15u) == 0)
-    hipLaunchKernelGGL(dfa_mask_kernel<true>, grid, dim3(kThreads), p.num_states * 256u * sizeof(uint32_t), st, p);
-  else
+  const bool lds = p.num_states <= kLdsStates && ((uintptr_t)p.trans & 15u) == 0;
+  const size_t lds_bytes = lds ? p.num_states * 256u * sizeof(uint32_t) : 0;
+  if (p.num_states <= kSetStates) {
+    const uint32_t per_block = (uint32_t)(kStTok * kThreads);
+    const dim3 grid((p.V + per_block - 1) / per_block, (batch + kStRows - 1) / kStRows);
+    if (p.num_states <= 8) launch_states<8>(p, grid, lds, lds_bytes, st);
+    else if (p.num_states <= 16) launch_states<16>(p, grid, lds, lds_bytes, st);
+    else launch_states<64>(p, grid, lds, lds_bytes, st);
+  } else {
+    const uint32_t per_block = (uint32_t)(kThreads * kTokPerThread);
+    const dim3 grid((p.V + per_block - 1) / per_block, (batch + kRowsPerBlock - 1) / kRowsPerBlock);
     hipLaunchKernelGGL(dfa_mask_kernel<false>, grid, dim3(kThreads), 0, st, p);
+  }
   return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }
 

@@ -154,7 +154,8 @@ def test_gpu_logit_masking_known_answer(torch_gpu):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("n,V,B", [(8, 1, 3), (8, 63, 5), (1, 64, 17), (20, 65, 16), (47, 1000, 33),
-                                   (60, 2049, 7), (120, 700, 20), (8, 128256, 128)])
+                                   (60, 2049, 7), (64, 3000, 9), (65, 3000, 9), (120, 700, 20),
+                                   (8, 128256, 128)])
 def test_gpu_dfa_mask_matches_oracle(torch_gpu, n, V, B):
     rng = np.random.default_rng(n * 1000 + V)
     table = random_dfa(rng, n, 0.4 if n > 2 else 0.9)
@@ -168,6 +169,17 @@ def test_gpu_dfa_mask_matches_oracle(torch_gpu, n, V, B):
     got = gpu_mask(torch_gpu, table, n, vocab, states)
     want = oracle.dfa_mask_host(table, n, off, by, states)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.gpu
+def test_gpu_dfa_mask_empty_table(torch_gpu):
+    # no states: every state is outside the table, so only tokens with no bytes are allowed
+    vocab = [b"", b"a", b"", b"{}", b"x" * 40]
+    off, by = pack(vocab)
+    states = np.array([0, 3, ERR], np.uint32)
+    got = gpu_mask(torch_gpu, np.zeros(0, np.uint32), 0, vocab, states)
+    np.testing.assert_array_equal(got, oracle.dfa_mask_host(np.zeros(0, np.uint32), 0, off, by, states))
+    assert got.tolist() == [[0b00101]] * 3
 
 
 @pytest.mark.gpu
