@@ -45,6 +45,7 @@ extern "C" {
 #define OXS_ERR_HIP (-4)            /* a HIP runtime call failed */
 #define OXS_ERR_UNSUPPORTED (-5)    /* a feature this build does not run on the GPU */
 #define OXS_ERR_NO_DEVICE (-6)
+#define OXS_ERR_TIMEOUT (-7)        /* oxs_host_wait gave up */
 
 /* Per-row outcome written to out_status[b]. */
 #define OXS_ROW_OK 0            /* Ok(token); token recorded (sampler.rs:387) */
@@ -260,6 +261,14 @@ int oxs_decode_step(oxs_sampler* sampler, const oxs_batch* batch, const oxs_deco
  * OXS_ERR_UNSUPPORTED when the device address would differ from the host's. */
 int oxs_host_alloc(size_t bytes, void** out);
 int oxs_host_free(void* ptr);
+
+/* Host side of the hand-off: spins until every one of `count` slots of
+ * oxs_decode_io.host_tokens carries a step count of at least `step` (modulo
+ * 2^32), copying each slot's token into tokens[i] as it reads it; no HIP call.
+ * A spin_limit of 0 waits without limit; otherwise OXS_ERR_TIMEOUT after that
+ * many passes. Replaces the host's wait on h_sampled_token's counter
+ * (megakernel_ops.cu:331-347). */
+int oxs_host_wait(const uint64_t* slots, uint32_t count, uint32_t step, uint32_t* tokens, uint64_t spin_limit);
 
 /*
  * Grammar masks from a DFA (the producer of oxs_batch.allowed_mask).

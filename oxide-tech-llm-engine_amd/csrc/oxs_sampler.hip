@@ -1976,6 +1976,7 @@ const char* oxs_status_string(int code) {
     case OXS_ERR_HIP: return "HIP runtime error";
     case OXS_ERR_UNSUPPORTED: return "unsupported on this device";
     case OXS_ERR_NO_DEVICE: return "no HIP device";
+    case OXS_ERR_TIMEOUT: return "timed out waiting for the device";
     default: return "unknown status";
   }
 }
@@ -2200,6 +2201,21 @@ int oxs_host_alloc(size_t bytes, void** out) {
 int oxs_host_free(void* ptr) {
   if (!ptr) return OXS_OK;
   return hipHostFree(ptr) == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+}
+
+int oxs_host_wait(const uint64_t* slots, uint32_t count, uint32_t step, uint32_t* tokens, uint64_t spin_limit) {
+  if (!slots || (count && !tokens)) return OXS_ERR_INVALID_ARGUMENT;
+  const volatile uint64_t* v = slots;
+  for (uint64_t spins = 0;; ++spins) {
+    uint32_t i = 0;
+    for (; i < count; ++i) {
+      const uint64_t x = v[i];  // one 8-byte load: the tag and its token together
+      if ((int32_t)((uint32_t)(x >> 32) - step) < 0) break;
+      tokens[i] = (uint32_t)x;
+    }
+    if (i == count) return OXS_OK;
+    if (spin_limit && spins >= spin_limit) return OXS_ERR_TIMEOUT;
+  }
 }
 
 }  // extern "C"

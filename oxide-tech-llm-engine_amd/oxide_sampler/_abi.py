@@ -21,6 +21,7 @@ OXS_ERR_LIMITS = -3
 OXS_ERR_HIP = -4
 OXS_ERR_UNSUPPORTED = -5
 OXS_ERR_NO_DEVICE = -6
+OXS_ERR_TIMEOUT = -7
 
 OXS_ROW_OK = 0
 OXS_ROW_EMPTY = 1
@@ -52,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "oxs_decode_step",
     "oxs_host_alloc",
     "oxs_host_free",
+    "oxs_host_wait",
     "oxs_dfa_mask",
     "oxs_dfa_mask_gather",
 )
@@ -199,6 +201,9 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_host_alloc.argtypes = [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]
     lib.oxs_host_free.restype = ctypes.c_int
     lib.oxs_host_free.argtypes = [ctypes.c_void_p]
+    lib.oxs_host_wait.restype = ctypes.c_int
+    lib.oxs_host_wait.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                  ctypes.c_uint64]
     lib.oxs_dfa_mask.restype = ctypes.c_int
     lib.oxs_dfa_mask.argtypes = [ctypes.POINTER(OxsDfa), ctypes.POINTER(OxsTokenBytes), ctypes.c_void_p,
                                  ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]

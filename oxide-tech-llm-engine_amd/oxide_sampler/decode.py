@@ -132,6 +132,7 @@ class DecodeLoop:
         self.io = OxsDecodeIo(self.current_token.data_ptr(), self.current_position.data_ptr(),
                               self.generated_count.data_ptr(), self._host)
         self.launched = 0  # steps launched; every step covers every slot
+        self._tokens = np.zeros(S, np.uint32)
         self.active: Dict[int, Sequence] = {}
         self._graph = None
 
@@ -219,16 +220,20 @@ class DecodeLoop:
         return int((self._slots.copy() >> np.uint64(32)).min())
 
     def wait(self, step: Optional[int] = None, timeout: float = 30.0) -> np.ndarray:
-        """Polls the host slots until every row carries step `step` (default:
-        the last launched), then returns the tokens of every slot; no stream
-        sync. Each slot is one 8-byte store, so its token belongs to its tag."""
+        """Polls the host slots (oxs_host_wait, in C) until every row carries
+        step `step` (default: the last launched), then returns the tokens of
+        every slot; no stream sync. Each slot is one 8-byte store, so its
+        token belongs to its tag."""
         want = (self.launched if step is None else int(step)) & 0xFFFFFFFF
         deadline = time.monotonic() + timeout
+        out = self._tokens
         while True:
-            snap = self._slots.copy()
-            tags = (snap >> np.uint64(32)).astype(np.int64)
-            if np.all(((tags - want) & 0xFFFFFFFF) < 0x80000000):
-                return (snap & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+            rc = self.lib.oxs_host_wait(ctypes.c_void_p(self._host), self.max_slots, want,
+                                        out.ctypes.data_as(ctypes.c_void_p), 1 << 20)
+            if rc == _abi.OXS_OK:
+                return out.copy()
+            if rc != _abi.OXS_ERR_TIMEOUT:
+                check(rc, "oxs_host_wait")
             if time.monotonic() > deadline:
                 raise TimeoutError(f"decode step {want} not finished after {timeout} s")
 

@@ -389,3 +389,22 @@ def test_gpu_decode_step_bf16_softcap_mask(torch_gpu, dtype, softcap):
     finally:
         t.cuda.synchronize()
         lib.oxs_host_free(host)
+
+
+def test_host_wait_reads_tagged_slots():
+    # oxs_host_wait makes no HIP call: plain host memory stands in for the mapped slots
+    lib = _abi.load_library()
+    tokens = np.zeros(4, np.uint32)
+    slots = np.array([(5 << 32) | 11, (5 << 32) | 22, (6 << 32) | 33, (5 << 32) | 44], np.uint64)
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    assert lib.oxs_host_wait(ptr(slots), 4, 5, ptr(tokens), 0) == _abi.OXS_OK
+    assert tokens.tolist() == [11, 22, 33, 44]
+    slots[1] = (4 << 32) | 99  # one row behind: times out after the spin limit
+    assert lib.oxs_host_wait(ptr(slots), 4, 5, ptr(tokens), 1000) == _abi.OXS_ERR_TIMEOUT
+    # step counts wrap modulo 2^32: 0xffffffff is behind 0, 1 is ahead of it
+    slots[:] = [(1 << 32) | 7, (0 << 32) | 8, (1 << 32) | 9, (0 << 32) | 10]
+    assert lib.oxs_host_wait(ptr(slots), 4, 0, ptr(tokens), 0) == _abi.OXS_OK
+    assert tokens.tolist() == [7, 8, 9, 10]
+    slots[2] = (0xFFFFFFFF << 32) | 9
+    assert lib.oxs_host_wait(ptr(slots), 4, 0, ptr(tokens), 10) == _abi.OXS_ERR_TIMEOUT
+    assert lib.oxs_host_wait(None, 4, 0, ptr(tokens), 10) == _abi.OXS_ERR_INVALID_ARGUMENT
