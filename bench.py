@@ -387,6 +387,27 @@ def summarize_pmc(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir):
     }
 
 
+def summarize_trace(folder):
+    """Average duration per launch of this library's kernels from a rocprofv3
+    --kernel-trace --stats folder (the *_kernel_stats.csv file)."""
+    import csv  # noqa: PLC0415
+    stats = next(Path(folder).glob("*kernel_stats.csv"))
+    out = {}
+    for r in csv.DictReader(open(stats)):
+        name = r["Name"]
+        for k in ("stream_kernel", "tail_kernel"):
+            if f"oxs::{k}<" in name and "<0" in name[name.index(k):name.index(k) + len(k) + 3]:
+                out[k] = {"avg_ns": float(r["AverageNs"]), "calls": int(r["Calls"]), "name": name}
+    return out
+
+
+def read_kernel_trace(path):
+    try:
+        return json.loads(Path(path).read_text()), str(path)
+    except (OSError, ValueError, KeyError):
+        return None, None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -403,7 +424,15 @@ def main():
                     help="sample: the headline config-2 line; decode / dfa_mask: secondary measurements")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="turn four rocprofv3 --pmc output folders into the traffic summary and exit")
+    ap.add_argument("--trace-summary", default=str(ROOT / "profiles" / "config2_kernel_trace.json"))
+    ap.add_argument("--summarize-trace", metavar="TRACE_DIR",
+                    help="turn a rocprofv3 --kernel-trace --stats folder of this bench into the per-kernel summary and exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summary = summarize_trace(args.summarize_trace)
+        Path(args.trace_summary).write_text(json.dumps(summary, indent=1) + "\n")
+        print(json.dumps(summary), flush=True)
+        return
     if args.summarize_pmc:
         summary = summarize_pmc(*args.summarize_pmc)
         Path(args.traffic_summary).write_text(json.dumps(summary, indent=1) + "\n")
@@ -568,6 +597,20 @@ def main():
         },
         "wall_s": wall,
     }
+    # The call is two kernels: the HBM-bound stream kernel moves the logits
+    # (everything but the tail's candidate lists and outputs); the tail is
+    # latency-bound. Their split, from the committed kernel trace of this bench.
+    split, split_src = read_kernel_trace(args.trace_summary)
+    if split and "stream_kernel" in split:
+        stream_bytes = B * (V * 4 + H * 4 + 104)
+        sk = split["stream_kernel"]["avg_ns"] * 1e-9
+        per = {"stream_kernel": {"avg_us": sk * 1e6, "algorithmic_bytes": stream_bytes,
+                                 "achieved": stream_bytes / sk / 1e9, "frac": stream_bytes / sk / 1e9 / HBM_PEAK_GBS,
+                                 "bound": "hbm"}}
+        if "tail_kernel" in split:
+            per["tail_kernel"] = {"avg_us": split["tail_kernel"]["avg_ns"] * 1e-3, "bound": "latency"}
+        result["roofline"]["per_kernel"] = per
+        result["roofline"]["per_kernel_source"] = split_src
     if achieved > 1.05 * HBM_PEAK_GBS:  # roofline.rs:53-style integrity check
         result["roofline"]["warning"] = "achieved exceeds 1.05 x peak: inputs were cached, not streamed"
     if not args.no_cpu:
