@@ -54,6 +54,9 @@ class TokenBytes:
     def __init__(self, vocab: Sequence[bytes], device: int = 0):
         t = _torch()
         lens = np.fromiter((len(b) for b in vocab), dtype=np.int64, count=len(vocab))
+        total = int(lens.sum()) if len(vocab) else 0
+        if total >= 1 << 32 or len(vocab) >= 1 << 31:
+            raise ValueError("token bytes are indexed with 32-bit offsets: at most 4 GiB and 2^31 tokens")
         offsets = np.zeros(len(vocab) + 1, np.uint32)
         if len(vocab):
             offsets[1:] = np.cumsum(lens).astype(np.uint32)
