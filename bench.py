@@ -89,16 +89,22 @@ def cpu_baseline(w, gpu_tokens, seconds):
     out = run(w.batch)  # warm-up and parity spot check on the whole batch
     t_batch = time.perf_counter() - t0
     match = bool(np.array_equal(out["tokens"], gpu_tokens)) if gpu_tokens is not None else None
-    reps = max(1, int(seconds / max(t_batch, 1e-6)))
-    t0 = time.perf_counter()
+    reps = max(5, int(seconds / max(t_batch, 1e-6)))
+    passes = []
     for _ in range(reps):
+        t0 = time.perf_counter()
         run(w.batch)
-    dt = time.perf_counter() - t0
+        passes.append(time.perf_counter() - t0)
+    dt = float(sum(passes))
     rows = reps * w.batch
     ncores = len(os.sched_getaffinity(0))
-    t0 = time.perf_counter()
-    run(w.batch, n_threads=min(ncores, w.batch))
-    dt_all = time.perf_counter() - t0
+    run(w.batch, n_threads=min(ncores, w.batch))  # warm-up of the thread pool
+    passes_all = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        run(w.batch, n_threads=min(ncores, w.batch))
+        passes_all.append(time.perf_counter() - t0)
+    dt_all = float(np.median(passes_all))
     cpu_model = platform.processor() or platform.machine()
     try:
         for line in open("/proc/cpuinfo"):
@@ -114,8 +120,9 @@ def cpu_baseline(w, gpu_tokens, seconds):
         "kind": "port",
         "sample": f"{rows} rows ({reps} passes over config-2 batch 0: B=64, V=128256 f32), 1 thread, rows in series",
         "us_per_row": dt / rows * 1e6,
+        "median_pass_s": float(np.median(passes)),
         "all_cores": {"value": w.batch / dt_all, "unit": "rows/s", "cores": min(ncores, w.batch),
-                      "sample": "one pass over config-2 batch 0, rows split statically"},
+                      "sample": "median of 5 passes over config-2 batch 0, rows split statically"},
         "cpu_model": cpu_model,
         "libc": " ".join(platform.libc_ver()),
         "tokens_match_gpu": match,
@@ -559,6 +566,19 @@ def main():
     elapsed_ms = ev0.elapsed_time(ev1)
     ms_per_step = elapsed_ms / steps
     rows_per_s = B * steps / (elapsed_ms / 1e3)
+    # the median per-step time: events between replays of the P-call graph
+    # (or between eager groups of P calls), outside the timed region above
+    groups = []
+    if graph is not None:
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(51)]
+        with torch.cuda.stream(stream):
+            evs[0].record(stream)
+            for i in range(50):
+                graph.replay()
+                evs[i + 1].record(stream)
+        torch.cuda.synchronize()
+        groups = [evs[i].elapsed_time(evs[i + 1]) * 1e3 / P for i in range(50)]
+    median_us = float(np.median(groups)) if groups else ms_per_step * 1e3
 
     alg = algorithmic_bytes(B, V, H, kept_avg)
     achieved = alg / (ms_per_step / 1e3) / 1e9
@@ -583,6 +603,7 @@ def main():
             "pool_bytes": P * B * V * 4, "launch": mode,
         },
         "tokens_per_s": rows_per_s,
+        "median_us_per_step": median_us,
         "achieved_GBps": achieved,
         "roofline": {
             "bound": "hbm",
