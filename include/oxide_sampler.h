@@ -136,7 +136,7 @@ typedef struct oxs_batch {
   const uint32_t* ban_ids;
 
   const uint32_t* allowed_mask; /* optional [B][mask_ld] words: bit (i%32) of word i/32 set = token i allowed */
-  int64_t mask_ld;
+  int64_t mask_ld;              /* >= ceil(vocab / 32), or 0: one mask shared by every row */
 
   uint32_t* history;      /* [B][history_ld] token ids (may be NULL when every history_len is 0 and nothing is recorded) */
   int64_t history_ld;
@@ -322,6 +322,39 @@ int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, const uint32
  */
 int oxs_dfa_mask_gather(const uint32_t* state_masks, uint32_t num_states, int64_t state_masks_ld, uint32_t vocab,
                         const uint32_t* states, uint32_t batch, uint32_t* mask, int64_t mask_ld, void* stream);
+
+/*
+ * Static grammar masks (one row, the same for every step), written as
+ * mask[ceil(vocab / 32)] words; pass them to oxs_batch with mask_ld = 0 to
+ * share them across rows.
+ *
+ * GbnfGrammarEngine::apply_grammar_mask (crates/oxide-core/src/sampler.rs:555-583)
+ * for the start rule: token t's text (tokens, UTF-8) is allowed when it is
+ * empty (no first character: the reference leaves it alone), when its first
+ * character, decoded from UTF-8 (a malformed sequence decodes to U+FFFD), lies
+ * in one of `ranges` ([lo, hi] code points, inclusive), or when a literal
+ * starts with its text or its text starts with a literal. All pointers device.
+ */
+typedef struct oxs_gbnf_rule {
+  uint32_t num_ranges;
+  const uint32_t* ranges;          /* [num_ranges][2] */
+  uint32_t num_literals;
+  const uint32_t* literal_offsets; /* [num_literals + 1] into literal_bytes */
+  const uint8_t* literal_bytes;
+} oxs_gbnf_rule;
+
+int oxs_gbnf_mask(const oxs_gbnf_rule* rule, const oxs_token_bytes* tokens, uint32_t* mask, void* stream);
+
+/*
+ * GrammarLogitMasker::mask_logits (crates/oxide-core/src/grammar_mask.rs:55-65):
+ * token t with an ASCII byte (token_ascii[t] < 256) is masked unless
+ * allowed_ascii[that byte] != 0; token_ascii[t] >= 256 stands for Rust's None
+ * (left alone). allowed_ascii is [256], token_ascii [vocab]; device pointers.
+ * The reference masks only min(vocab_ascii_bytes.len(), logits.len()) tokens:
+ * pass that count as vocab.
+ */
+int oxs_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, uint32_t vocab, uint32_t* mask,
+                   void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

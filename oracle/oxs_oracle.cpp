@@ -502,3 +502,61 @@ void oxo_dfa_mask(const uint32_t* transitions, uint32_t num_states, const uint32
     }
   }
 }
+
+// The first character of UTF-8 text (text.chars().next()); U+FFFD for a
+// malformed sequence (bad or missing continuation, overlong form, surrogate,
+// beyond U+10FFFF), as String::from_utf8_lossy would give.
+static uint32_t utf8_first(const uint8_t* b, uint32_t len) {
+  const uint32_t c0 = b[0];
+  if (c0 < 0x80) return c0;
+  uint32_t need, c;
+  if (c0 >= 0xc0 && c0 < 0xe0) { need = 1; c = c0 & 0x1f; }
+  else if (c0 >= 0xe0 && c0 < 0xf0) { need = 2; c = c0 & 0x0f; }
+  else if (c0 >= 0xf0 && c0 < 0xf8) { need = 3; c = c0 & 0x07; }
+  else return 0xfffd;
+  if (len <= need) return 0xfffd;
+  for (uint32_t i = 1; i <= need; ++i) {
+    if ((b[i] & 0xc0) != 0x80) return 0xfffd;
+    c = (c << 6) | (b[i] & 0x3f);
+  }
+  static const uint32_t kLeast[4] = {0, 0x80, 0x800, 0x10000};  // shortest form of each length
+  if (c < kLeast[need] || (c >= 0xd800 && c <= 0xdfff) || c > 0x10ffff) return 0xfffd;
+  return c;
+}
+
+// GbnfGrammarEngine::apply_grammar_mask (sampler.rs:555-583), one row.
+void oxo_gbnf_mask(const uint32_t* ranges, uint32_t num_ranges, const uint32_t* lit_off, const uint8_t* lit_bytes,
+                   uint32_t num_lits, const uint32_t* offsets, const uint8_t* bytes, uint32_t num_bytes,
+                   uint32_t vocab, uint32_t* mask) {
+  for (uint32_t w = 0; w < (vocab + 31) / 32; ++w) mask[w] = 0;
+  for (uint32_t t = 0; t < vocab; ++t) {
+    const uint32_t lo = offsets[t], hi = offsets[t + 1];
+    if (hi < lo || hi > num_bytes) continue;
+    const uint32_t len = hi - lo;
+    bool allowed;
+    if (len == 0) {
+      allowed = true;  // no first character: :560 skips the token
+    } else {
+      const uint32_t c = utf8_first(bytes + lo, len);
+      allowed = false;
+      for (uint32_t i = 0; i < num_ranges && !allowed; ++i)  // :561-567
+        if (c >= ranges[2 * i] && c <= ranges[2 * i + 1]) allowed = true;
+      for (uint32_t i = 0; i < num_lits && !allowed; ++i) {  // :568-575
+        const uint32_t ll = lit_off[i + 1] - lit_off[i];
+        const bool lit_starts_with_text = len <= ll && memcmp(lit_bytes + lit_off[i], bytes + lo, len) == 0;
+        const bool text_starts_with_lit = ll <= len && memcmp(bytes + lo, lit_bytes + lit_off[i], ll) == 0;
+        allowed = lit_starts_with_text || text_starts_with_lit;
+      }
+    }
+    if (allowed) mask[t / 32] |= 1u << (t % 32);
+  }
+}
+
+// GrammarLogitMasker::mask_logits (grammar_mask.rs:55-65), one row.
+void oxo_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, uint32_t vocab, uint32_t* mask) {
+  for (uint32_t w = 0; w < (vocab + 31) / 32; ++w) mask[w] = 0;
+  for (uint32_t t = 0; t < vocab; ++t) {
+    const bool masked = token_ascii[t] < 256 && !allowed_ascii[token_ascii[t]];  // is_some_and(!allowed)
+    if (!masked) mask[t / 32] |= 1u << (t % 32);
+  }
+}

@@ -92,6 +92,13 @@ void oxo_dfa_mask(const uint32_t* transitions, uint32_t num_states, const uint32
                   const uint8_t* bytes, uint32_t num_bytes, uint32_t vocab, const uint32_t* states,
                   uint32_t batch, uint32_t* mask, int64_t mask_ld);
 
+/* The static masks of oxs_gbnf_mask (sampler.rs:555-583) and oxs_ascii_mask
+ * (grammar_mask.rs:55-65), host pointers, one row of ceil(vocab / 32) words. */
+void oxo_gbnf_mask(const uint32_t* ranges, uint32_t num_ranges, const uint32_t* lit_off, const uint8_t* lit_bytes,
+                   uint32_t num_lits, const uint32_t* offsets, const uint8_t* bytes, uint32_t num_bytes,
+                   uint32_t vocab, uint32_t* mask);
+void oxo_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, uint32_t vocab, uint32_t* mask);
+
 /* glibc's expf etc., exported so tests can compare the device emulation. */
 float oxo_expf(float x);
 float oxo_logf(float x);

@@ -54,6 +54,11 @@ def load() -> ctypes.CDLL:
     lib.oxo_decode_step.argtypes = [vp, vp, ctypes.c_int]
     lib.oxo_raw_argmax.restype = ctypes.c_uint32
     lib.oxo_raw_argmax.argtypes = [vp, ctypes.c_uint32]
+    lib.oxo_gbnf_mask.restype = None
+    lib.oxo_gbnf_mask.argtypes = [vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32,
+                                  ctypes.c_uint32, vp]
+    lib.oxo_ascii_mask.restype = None
+    lib.oxo_ascii_mask.argtypes = [vp, vp, ctypes.c_uint32, vp]
     lib.oxo_dfa_mask.restype = None
     lib.oxo_dfa_mask.argtypes = [vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32,
                                  vp, ctypes.c_int64]
@@ -67,7 +72,7 @@ def _ptr(a):
 
 def sample_batch_host(abi, *, logits, dtype, configs_bytes, bias_ids, bias_values, ban_ids, mask, history,
                       history_len, history_cap, record, uniforms, rng_state, mu, kept_ld, logits_out=None,
-                      shared_config=False, n_threads=1, decode=None, kept_fill=0, softcap=0.0):
+                      shared_config=False, n_threads=1, decode=None, kept_fill=0, softcap=0.0, shared_mask=False):
     """Runs the oracle over host numpy arrays with the oxs_batch descriptor.
 
     `abi` is the product's ctypes module (for the OxsBatch layout). Mutable
@@ -98,7 +103,7 @@ def sample_batch_host(abi, *, logits, dtype, configs_bytes, bias_ids, bias_value
     b.ban_ids = _ptr(ban_ids) if ban_ids is not None and ban_ids.size else None
     if mask is not None:
         b.allowed_mask = mask.ctypes.data
-        b.mask_ld = mask.shape[1]
+        b.mask_ld = 0 if shared_mask else mask.shape[1]  # 0: row 0 for every row
     if history is not None:
         b.history = history.ctypes.data
         b.history_ld = history.shape[1]
@@ -193,3 +198,38 @@ def raw_argmax_host(row) -> int:
     """oxo_raw_argmax on one f32 row (continuous_batching.rs:961-970)."""
     row = np.ascontiguousarray(row, dtype=np.float32)
     return int(load().oxo_raw_argmax(_ptr(row), row.shape[0]))
+
+
+def _pack_strings(items):
+    data = [bytes(x) for x in items]
+    off = np.zeros(len(data) + 1, np.uint32)
+    if data:
+        off[1:] = np.cumsum([len(d) for d in data])
+    flat = np.frombuffer(b"".join(data), np.uint8).copy() if data else np.zeros(0, np.uint8)
+    return off, flat
+
+
+def gbnf_mask_host(ranges, literals, offsets, byte_arr):
+    """The oracle's GBNF start-rule mask: ranges [(lo, hi) code points], literals [bytes]."""
+    lib = load()
+    r = np.asarray(ranges, np.uint32).reshape(-1)
+    loff, lbytes = _pack_strings(literals)
+    offsets = np.ascontiguousarray(offsets, dtype=np.uint32)
+    byte_arr = np.ascontiguousarray(byte_arr, dtype=np.uint8)
+    vocab = offsets.shape[0] - 1
+    mask = np.zeros(max((vocab + 31) // 32, 1), np.uint32)
+    lib.oxo_gbnf_mask(_ptr(r) if r.size else None, r.size // 2, _ptr(loff), _ptr(lbytes) if lbytes.size else None,
+                      len(literals), _ptr(offsets), _ptr(byte_arr) if byte_arr.size else None, byte_arr.shape[0],
+                      vocab, _ptr(mask))
+    return mask[: (vocab + 31) // 32]
+
+
+def ascii_mask_host(allowed, token_ascii):
+    """The oracle's ASCII masker row: allowed [256] bools, token_ascii [vocab] (>= 256 for None)."""
+    lib = load()
+    a = np.ascontiguousarray(allowed, dtype=np.uint8)
+    ta = np.ascontiguousarray(token_ascii, dtype=np.uint16)
+    vocab = ta.shape[0]
+    mask = np.zeros(max((vocab + 31) // 32, 1), np.uint32)
+    lib.oxo_ascii_mask(_ptr(a), _ptr(ta), vocab, _ptr(mask))
+    return mask[: (vocab + 31) // 32]

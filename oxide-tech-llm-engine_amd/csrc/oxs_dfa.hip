@@ -254,6 +254,97 @@ __global__ __launch_bounds__(kThreads) void mask_gather_kernel(const uint32_t* _
   }
 }
 
+// ---------------------------------------------------------------- static masks
+
+// The first character of a token's text, decoded from UTF-8 (Rust's
+// text.chars().next()); a malformed sequence (bad continuation, truncation,
+// overlong form, surrogate, beyond U+10FFFF) gives U+FFFD, as a lossy decode
+// would (the reference's vocabulary is always valid UTF-8).
+__device__ __forceinline__ uint32_t first_char(const uint8_t* b, uint32_t len) {
+  const uint32_t c0 = b[0];
+  if (c0 < 0x80u) return c0;
+  uint32_t n, c;
+  if ((c0 & 0xe0u) == 0xc0u) { n = 1; c = c0 & 0x1fu; }
+  else if ((c0 & 0xf0u) == 0xe0u) { n = 2; c = c0 & 0x0fu; }
+  else if ((c0 & 0xf8u) == 0xf0u) { n = 3; c = c0 & 0x07u; }
+  else return 0xfffdu;
+  if (len < n + 1) return 0xfffdu;
+  for (uint32_t i = 1; i <= n; ++i) {
+    const uint32_t ci = b[i];
+    if ((ci & 0xc0u) != 0x80u) return 0xfffdu;
+    c = (c << 6) | (ci & 0x3fu);
+  }
+  const uint32_t least = n == 1 ? 0x80u : n == 2 ? 0x800u : 0x10000u;
+  if (c < least || (c >= 0xd800u && c <= 0xdfffu) || c > 0x10ffffu) return 0xfffdu;
+  return c;
+}
+
+__device__ __forceinline__ void write_mask_bits(bool ok, uint32_t t, uint32_t words, uint32_t* mask) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint64_t m = __ballot(ok);
+  const uint32_t wbase = (t - lane) / 32u;
+  if (lane == 0 && wbase < words) mask[wbase] = (uint32_t)m;
+  if (lane == 32 && wbase + 1 < words) mask[wbase + 1] = (uint32_t)(m >> 32);
+}
+
+struct GbnfParams {
+  const uint32_t* ranges;  // [n_ranges][2]
+  uint32_t n_ranges;
+  const uint32_t* lit_off;  // [n_lits + 1]
+  const uint8_t* lit_bytes;
+  uint32_t n_lits;
+  const uint32_t* offsets;
+  const uint8_t* bytes;
+  uint32_t num_bytes;
+  uint32_t V;
+  uint32_t* mask;
+};
+
+// GbnfGrammarEngine::apply_grammar_mask (crates/oxide-core/src/sampler.rs:555-583):
+// a token with no characters is left alone; otherwise it is allowed when its
+// first character lies in one of the rule's ranges, or when a literal starts
+// with its text or its text starts with a literal. One thread per token.
+__global__ __launch_bounds__(kThreads) void gbnf_mask_kernel(const GbnfParams p) {
+  const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+  bool ok = false;
+  if (t < p.V) {
+    const uint32_t b0 = p.offsets[t], e = p.offsets[t + 1];
+    if (e >= b0 && e <= p.num_bytes) {
+      const uint32_t len = e - b0;
+      const uint8_t* tb = p.bytes + b0;
+      if (len == 0) {
+        ok = true;  // text.chars().next() is None: not masked
+      } else {
+        const uint32_t c = first_char(tb, len);
+        for (uint32_t i = 0; i < p.n_ranges && !ok; ++i) ok = c >= p.ranges[2 * i] && c <= p.ranges[2 * i + 1];
+        for (uint32_t i = 0; i < p.n_lits && !ok; ++i) {
+          const uint32_t lb = p.lit_off[i], ll = p.lit_off[i + 1] - lb;
+          const uint32_t n = min(ll, len);  // lit.starts_with(text) || text.starts_with(lit): equal first n bytes
+          bool same = true;
+          for (uint32_t j = 0; j < n && same; ++j) same = p.lit_bytes[lb + j] == tb[j];
+          ok = same;
+        }
+      }
+    }
+  }
+  write_mask_bits(ok, t, (p.V + 31u) / 32u, p.mask);
+}
+
+// GrammarLogitMasker::mask_logits (crates/oxide-core/src/grammar_mask.rs:55-65):
+// a token whose byte b is given (token_ascii[t] < 256) is masked unless
+// allowed[b]; a token without one (Rust's None) is left alone.
+__global__ __launch_bounds__(kThreads) void ascii_mask_kernel(const uint8_t* __restrict__ allowed,
+                                                             const uint16_t* __restrict__ token_ascii, uint32_t V,
+                                                             uint32_t* __restrict__ mask) {
+  const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+  bool ok = false;
+  if (t < V) {
+    const uint32_t b = token_ascii[t];
+    ok = b >= 256u || allowed[b] != 0;
+  }
+  write_mask_bits(ok, t, (V + 31u) / 32u, mask);
+}
+
 }  // namespace oxs_grammar
 
 extern "C" int oxs_dfa_mask(const oxs_dfa* dfa, const oxs_token_bytes* tokens, const uint32_t* states,
@@ -308,5 +399,40 @@ extern "C" int oxs_dfa_mask_gather(const uint32_t* state_masks, uint32_t num_sta
   const dim3 grid((words + kGatherWords - 1) / kGatherWords, batch);
   hipLaunchKernelGGL(mask_gather_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, state_masks, num_states,
                      state_masks_ld, words, states, mask, mask_ld);
+  return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+}
+
+extern "C" int oxs_gbnf_mask(const oxs_gbnf_rule* rule, const oxs_token_bytes* tokens, uint32_t* mask,
+                             void* stream) {
+  using namespace oxs_grammar;
+  if (!rule || !tokens) return OXS_ERR_INVALID_ARGUMENT;
+  if (tokens->vocab == 0) return OXS_OK;
+  if (!tokens->offsets || !tokens->bytes || !mask || (rule->num_ranges && !rule->ranges) ||
+      (rule->num_literals && (!rule->literal_offsets || !rule->literal_bytes)))
+    return OXS_ERR_INVALID_ARGUMENT;
+  if (tokens->vocab > (1u << 31)) return OXS_ERR_INVALID_ARGUMENT;
+  GbnfParams p;
+  p.ranges = rule->ranges;
+  p.n_ranges = rule->num_ranges;
+  p.lit_off = rule->literal_offsets;
+  p.lit_bytes = rule->literal_bytes;
+  p.n_lits = rule->num_literals;
+  p.offsets = tokens->offsets;
+  p.bytes = tokens->bytes;
+  p.num_bytes = tokens->num_bytes;
+  p.V = tokens->vocab;
+  p.mask = mask;
+  hipLaunchKernelGGL(gbnf_mask_kernel, dim3((p.V + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                     (hipStream_t)stream, p);
+  return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+}
+
+extern "C" int oxs_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, uint32_t vocab,
+                              uint32_t* mask, void* stream) {
+  using namespace oxs_grammar;
+  if (vocab == 0) return OXS_OK;
+  if (!allowed_ascii || !token_ascii || !mask || vocab > (1u << 31)) return OXS_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(ascii_mask_kernel, dim3((vocab + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                     (hipStream_t)stream, allowed_ascii, token_ascii, vocab, mask);
   return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }

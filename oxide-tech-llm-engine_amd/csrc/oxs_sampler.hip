@@ -2088,7 +2088,8 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
   if (!b->logits || !b->configs || !b->out_tokens) return OXS_ERR_INVALID_ARGUMENT;
   if (b->logits_dtype != OXS_DTYPE_F32 && b->logits_dtype != OXS_DTYPE_BF16) return OXS_ERR_INVALID_ARGUMENT;
   if (b->logits_ld < (int64_t)b->vocab) return OXS_ERR_INVALID_ARGUMENT;
-  if (b->allowed_mask && b->mask_ld < (int64_t)((b->vocab + 31) / 32)) return OXS_ERR_INVALID_ARGUMENT;
+  if (b->allowed_mask && b->mask_ld != 0 && b->mask_ld < (int64_t)((b->vocab + 31) / 32))
+    return OXS_ERR_INVALID_ARGUMENT;  // 0: one mask for every row
   if (!b->uniforms && !b->rng_state) return OXS_ERR_INVALID_ARGUMENT;
   if (b->history && (!b->history_len || b->history_ld <= 0)) return OXS_ERR_INVALID_ARGUMENT;
   if (b->flags & OXS_FLAG_RECORD_HISTORY) {

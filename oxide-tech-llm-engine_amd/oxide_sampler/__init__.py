@@ -25,7 +25,7 @@ from .engine import (
     ShapeMismatch,
     configs_to_array,
 )
-from .grammar import DfaSchemaGrammar, SchemaMismatch, TokenBytes
+from .grammar import DfaSchemaGrammar, GbnfGrammarEngine, GbnfRule, GrammarLogitMasker, SchemaMismatch, TokenBytes
 from .decode import DecodeLoop, TokenEvent
 from ._abi import (
     LibraryMissing,
@@ -42,6 +42,9 @@ __all__ = [
     "ShapeMismatch",
     "configs_to_array",
     "DfaSchemaGrammar",
+    "GbnfGrammarEngine",
+    "GbnfRule",
+    "GrammarLogitMasker",
     "SchemaMismatch",
     "TokenBytes",
     "DecodeLoop",

@@ -56,6 +56,8 @@ EXPORTED_SYMBOLS = (
     "oxs_host_wait",
     "oxs_dfa_mask",
     "oxs_dfa_mask_gather",
+    "oxs_gbnf_mask",
+    "oxs_ascii_mask",
 )
 
 OXS_DFA_ERROR_STATE = 0xFFFFFFFF
@@ -149,6 +151,16 @@ class OxsTokenBytes(ctypes.Structure):
     ]
 
 
+class OxsGbnfRule(ctypes.Structure):
+    _fields_ = [
+        ("num_ranges", ctypes.c_uint32),
+        ("ranges", ctypes.c_void_p),
+        ("num_literals", ctypes.c_uint32),
+        ("literal_offsets", ctypes.c_void_p),
+        ("literal_bytes", ctypes.c_void_p),
+    ]
+
+
 class OxsDecodeIo(ctypes.Structure):
     _fields_ = [
         ("current_token", ctypes.c_void_p),
@@ -211,6 +223,12 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_dfa_mask_gather.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int64, ctypes.c_uint32,
                                         ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int64,
                                         ctypes.c_void_p]
+    lib.oxs_gbnf_mask.restype = ctypes.c_int
+    lib.oxs_gbnf_mask.argtypes = [ctypes.POINTER(OxsGbnfRule), ctypes.POINTER(OxsTokenBytes), ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    lib.oxs_ascii_mask.restype = ctypes.c_int
+    lib.oxs_ascii_mask.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+                                   ctypes.c_void_p]
     if lib.oxs_abi_version() != OXS_ABI_VERSION:
         raise RuntimeError(f"liboxide_sampler ABI {lib.oxs_abi_version()} != {OXS_ABI_VERSION}")
     if path is None:

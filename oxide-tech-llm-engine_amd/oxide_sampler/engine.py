@@ -243,7 +243,7 @@ class BatchSampler:
             b.ban_ids = ban_ids.data_ptr()
         if mask is not None:
             b.allowed_mask = mask.data_ptr()
-            b.mask_ld = int(mask.stride(0))
+            b.mask_ld = int(mask.stride(0)) if mask.dim() == 2 else 0  # a 1-D mask is shared by every row
         if history is not None:
             b.history = history.data_ptr()
             b.history_ld = int(history.stride(0))

@@ -14,6 +14,10 @@ crates/oxide-server/src/dfa.rs). Its token masks run on the GPU through
   states)`: the same masks from a per-state table computed once per grammar and
   vocabulary (`oxs_dfa_mask_gather`), for decode loops.
 
+The two static maskers of the reference are mirrored the same way:
+`GbnfGrammarEngine` (sampler.rs:523-585; `oxs_gbnf_mask`) and
+`GrammarLogitMasker` (grammar_mask.rs:17-66; `oxs_ascii_mask`).
+
 `transition`, `deterministic_transition` and `find_jump_forward_bytes` walk the
 table on the host, as the reference does (dfa.rs:110-190): they are single
 lookups, not a data-parallel path.
@@ -21,12 +25,13 @@ lookups, not a data-parallel path.
 from __future__ import annotations
 
 import ctypes
-from typing import List, Optional, Sequence, Tuple
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
 from . import _abi
-from ._abi import OxsDfa, OxsTokenBytes, check, load_library
+from ._abi import OxsDfa, OxsGbnfRule, OxsTokenBytes, check, load_library
 
 DFA_ERROR_STATE = _abi.OXS_DFA_ERROR_STATE
 
@@ -222,15 +227,129 @@ class DfaSchemaGrammar:
 
     def apply_dfa_mask(self, current_state: int, token_bytes, logits) -> None:
         """dfa.rs:130-148: tokens whose bytes do not walk from current_state get -inf (in place)."""
-        t = _torch()
         tb = token_bytes if isinstance(token_bytes, TokenBytes) else TokenBytes(list(token_bytes))
-        words = self.token_masks(tb, [current_state])[0].cpu().numpy().view(np.uint32)
-        bits = np.unpackbits(words.view(np.uint8), bitorder="little")[: tb.vocab].astype(bool)
-        n = min(tb.vocab, len(logits))
-        if hasattr(logits, "masked_fill_"):
-            allowed = t.from_numpy(bits[:n].copy()).to(logits.device)
-            logits[:n].masked_fill_(~allowed, float("-inf"))
-        else:
-            for i in range(n):
-                if not bits[i]:
-                    logits[i] = float("-inf")
+        _mask_in_place(logits, self.token_masks(tb, [current_state])[0], tb.vocab)
+
+
+def _mask_in_place(logits, words, vocab: int) -> None:
+    """-inf into `logits` (list, numpy array or torch tensor) where the packed row `words` has a 0 bit."""
+    t = _torch()
+    w = words.cpu().numpy().view(np.uint32)
+    bits = np.unpackbits(w.view(np.uint8), bitorder="little")[:vocab].astype(bool)
+    n = min(vocab, len(logits))
+    if hasattr(logits, "masked_fill_"):
+        allowed = t.from_numpy(bits[:n].copy()).to(logits.device)
+        logits[:n].masked_fill_(~allowed, float("-inf"))
+    else:
+        for i in range(n):
+            if not bits[i]:
+                logits[i] = float("-inf")
+
+
+@dataclass
+class GbnfRule:
+    """GbnfRule (crates/oxide-core/src/sampler.rs:523-529)."""
+
+    rule_name: str
+    allowed_char_ranges: List[Tuple[str, str]] = field(default_factory=list)
+    literal_strings: List[str] = field(default_factory=list)
+
+
+class GbnfGrammarEngine:
+    """GbnfGrammarEngine (sampler.rs:531-585): rules by name and a start rule.
+    Its mask is one static row (oxs_gbnf_mask on the GPU)."""
+
+    def __init__(self, rules: Dict[str, GbnfRule], start_rule: str):
+        self.rules = dict(rules)
+        self.start_rule = start_rule
+
+    @classmethod
+    def new_json_grammar(cls) -> "GbnfGrammarEngine":
+        """sampler.rs:539-553."""
+        root = GbnfRule("root", [("{", "{"), ("[", "["), ('"', '"')], ["true", "false", "null"])
+        return cls({"root": root}, "root")
+
+    def token_mask(self, vocab_tokens, device: int = 0, stream=None):
+        """Packed mask (int32 [ceil(vocab / 32)] on the GPU) of the start rule,
+        or None when the start rule is missing (the reference then masks nothing)."""
+        rule = self.rules.get(self.start_rule)
+        if rule is None:
+            return None
+        t = _torch()
+        lib = load_library()
+        dev = t.device("cuda", device)
+        tb = vocab_tokens if isinstance(vocab_tokens, TokenBytes) else TokenBytes(
+            [str(x).encode("utf-8") for x in vocab_tokens], device)
+        ranges = np.array([[ord(a), ord(b)] for a, b in rule.allowed_char_ranges], np.uint32).reshape(-1)
+        lits = [x.encode("utf-8") for x in rule.literal_strings]
+        loff = np.zeros(len(lits) + 1, np.uint32)
+        if lits:
+            loff[1:] = np.cumsum([len(x) for x in lits])
+        lbytes = np.frombuffer(b"".join(lits), np.uint8).copy() if lits else np.zeros(1, np.uint8)
+        d_ranges = t.from_numpy(ranges.view(np.int32).copy() if ranges.size else np.zeros(2, np.int32)).to(dev)
+        d_loff = t.from_numpy(loff.view(np.int32).copy()).to(dev)
+        d_lbytes = t.from_numpy(lbytes if lbytes.size else np.zeros(1, np.uint8)).to(dev)
+        words = (tb.vocab + 31) // 32
+        mask = t.zeros(max(words, 1), dtype=t.int32, device=dev)
+        r = OxsGbnfRule(ranges.size // 2, d_ranges.data_ptr(), len(lits), d_loff.data_ptr(), d_lbytes.data_ptr())
+        s = stream if stream is not None else t.cuda.current_stream(dev)
+        check(lib.oxs_gbnf_mask(ctypes.byref(r), ctypes.byref(tb.as_c()), ctypes.c_void_p(mask.data_ptr()),
+                                ctypes.c_void_p(s.cuda_stream)), "oxs_gbnf_mask")
+        s.synchronize()  # the argument buffers above are freed on return
+        return mask[:words]
+
+    def apply_grammar_mask(self, logits, vocab_tokens) -> None:
+        """sampler.rs:556-584: disallowed tokens' logits become -inf (in place)."""
+        m = self.token_mask(vocab_tokens)
+        if m is not None:
+            _mask_in_place(logits, m, len(vocab_tokens) if not isinstance(vocab_tokens, TokenBytes)
+                           else vocab_tokens.vocab)
+
+
+class GrammarLogitMasker:
+    """GrammarLogitMasker (crates/oxide-core/src/grammar_mask.rs:17-66): an
+    allowed-byte table over token ASCII bytes. Its mask runs on the GPU
+    (oxs_ascii_mask)."""
+
+    def __init__(self):
+        mask = [False] * 256  # Default (grammar_mask.rs:23-35): printable ASCII, newline and tab
+        for b in range(0x20, 0x7F):
+            mask[b] = True
+        mask[ord("\n")] = True
+        mask[ord("\t")] = True
+        self.allowed_ascii_mask = mask
+        self.is_active = True
+
+    @classmethod
+    def new(cls) -> "GrammarLogitMasker":
+        return cls()
+
+    def restrict_to_numbers(self) -> None:
+        """grammar_mask.rs:43-52."""
+        self.allowed_ascii_mask = [False] * 256
+        for b in b"0123456789.-,}]":
+            self.allowed_ascii_mask[b] = True
+
+    def token_mask(self, vocab_ascii_bytes: Sequence[Optional[int]], device: int = 0, stream=None):
+        """Packed mask (int32 [ceil(n / 32)] on the GPU) of the first n tokens."""
+        t = _torch()
+        lib = load_library()
+        dev = t.device("cuda", device)
+        n = len(vocab_ascii_bytes)
+        codes = np.array([256 if b is None else int(b) for b in vocab_ascii_bytes], np.uint16)
+        allowed = t.tensor([1 if a else 0 for a in self.allowed_ascii_mask], dtype=t.uint8, device=dev)
+        d_codes = t.from_numpy(codes.view(np.int16).copy() if n else np.zeros(1, np.int16)).to(dev)
+        words = (n + 31) // 32
+        mask = t.zeros(max(words, 1), dtype=t.int32, device=dev)
+        s = stream if stream is not None else t.cuda.current_stream(dev)
+        check(lib.oxs_ascii_mask(ctypes.c_void_p(allowed.data_ptr()), ctypes.c_void_p(d_codes.data_ptr()), n,
+                                 ctypes.c_void_p(mask.data_ptr()), ctypes.c_void_p(s.cuda_stream)), "oxs_ascii_mask")
+        s.synchronize()
+        return mask[:words]
+
+    def mask_logits(self, vocab_ascii_bytes: Sequence[Optional[int]], logits) -> None:
+        """grammar_mask.rs:55-65: tokens with a disallowed byte get -inf (in place)."""
+        if not self.is_active:
+            return
+        n = min(len(vocab_ascii_bytes), len(logits))
+        _mask_in_place(logits, self.token_mask(list(vocab_ascii_bytes)[:n]), n)

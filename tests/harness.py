@@ -31,7 +31,8 @@ class Result:
 
 
 def run_oracle(w: Workload, kept_ld: int = 256, record: bool = True, use_rng: bool = False,
-               rng_state: Optional[np.ndarray] = None, logits_out: bool = False, n_threads: int = 1) -> Result:
+               rng_state: Optional[np.ndarray] = None, logits_out: bool = False, n_threads: int = 1,
+               shared_mask: bool = False) -> Result:
     cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
     history = w.history.copy()
     hist_len = w.history_len.copy()
@@ -43,7 +44,7 @@ def run_oracle(w: Workload, kept_ld: int = 256, record: bool = True, use_rng: bo
         bias_values=bias_vals, ban_ids=ban_ids, mask=w.mask, history=history, history_len=hist_len,
         history_cap=history.shape[1], record=record, uniforms=None if use_rng else w.uniforms,
         rng_state=rng, mu=mu, kept_ld=kept_ld, logits_out=lo, n_threads=n_threads,
-        softcap=float(w.extra.get("softcap", 0.0)))
+        softcap=float(w.extra.get("softcap", 0.0)), shared_mask=shared_mask)
     return Result(out["tokens"], out["status"], out["kept_count"], out["kept_ids"][:, :kept_ld],
                   out["kept_probs"][:, :kept_ld], history, hist_len, mu, rng, lo)
 
@@ -73,7 +74,7 @@ def to_device(w: Workload, torch):
 
 def run_gpu(w: Workload, torch, kept_ld: int = 256, record: bool = True, use_rng: bool = False,
             rng_state: Optional[np.ndarray] = None, logits_out: bool = False, logits_dev=None,
-            max_top_k: int = 256) -> Result:
+            max_top_k: int = 256, shared_mask: bool = False) -> Result:
     d = torch.device("cuda")
     cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
     s = gpu_sampler(w.batch, w.vocab, max_top_k)
@@ -83,6 +84,8 @@ def run_gpu(w: Workload, torch, kept_ld: int = 256, record: bool = True, use_rng
     mu = torch.from_numpy(w.mu.copy()).to(d) if w.mu is not None else None
     rng = torch.from_numpy(rng_state.view(np.int64).copy()).to(d) if rng_state is not None else None
     mask = torch.from_numpy(w.mask.view(np.int32)).to(d) if w.mask is not None else None
+    if mask is not None and shared_mask:
+        mask = mask[0].contiguous()  # 1-D: one mask for every row (mask_ld = 0)
     lo = torch.empty(w.batch, w.vocab, dtype=torch.float32, device=d) if logits_out else None
     out = s.sample(
         logits, torch.from_numpy(cfg).to(d),
