@@ -92,7 +92,8 @@ def test_create_rejects_bad_arguments_without_a_device(lib):
     assert lib.oxs_sampler_destroy(None) in (_abi.OXS_OK, _abi.OXS_ERR_INVALID_ARGUMENT)
 
 
-_STRUCTS = ("oxs_sampling_config", "oxs_limits", "oxs_batch", "oxs_decode_io", "oxs_dfa", "oxs_token_bytes")
+_STRUCTS = ("oxs_sampling_config", "oxs_limits", "oxs_batch", "oxs_decode_io", "oxs_dfa", "oxs_token_bytes",
+            "oxs_gbnf_rule")
 
 
 def _c_layouts(tmp_path):
@@ -122,7 +123,8 @@ def _c_layouts(tmp_path):
 def test_ctypes_structs_match_the_header_layout(tmp_path):
     # every struct the Python binding passes through the ABI, field by field
     py = {"oxs_sampling_config": _abi.OxsSamplingConfig, "oxs_limits": _abi.OxsLimits, "oxs_batch": _abi.OxsBatch,
-          "oxs_decode_io": _abi.OxsDecodeIo, "oxs_dfa": _abi.OxsDfa, "oxs_token_bytes": _abi.OxsTokenBytes}
+          "oxs_decode_io": _abi.OxsDecodeIo, "oxs_dfa": _abi.OxsDfa, "oxs_token_bytes": _abi.OxsTokenBytes,
+          "oxs_gbnf_rule": _abi.OxsGbnfRule}
     fields, c = _c_layouts(tmp_path)
     for name, cls in py.items():
         assert [f for f, _ in cls._fields_] == fields[name], name
