@@ -256,6 +256,22 @@ typedef struct oxs_decode_io {
  */
 int oxs_decode_step(oxs_sampler* sampler, const oxs_batch* batch, const oxs_decode_io* io, void* stream);
 
+/*
+ * Batched argmax, replacing launch_cuda_argmax(const float*, int vocab_size,
+ * uint32_t* out_token, float* out_max_val, int batch_size, cudaStream_t)
+ * (oxide-backend-cuda/src/kernels/sampling_dfa.cu:161-178; driver.rs:671-679),
+ * the CUDA backend's greedy path (oxide-backend-cuda/src/lib.rs:2479, :3266,
+ * :4063). For each row of logits [batch][logits_ld] (f32, device): the largest
+ * value above -1e30 and its token id, NaN and values <= -1e30 never taken (the
+ * reference's running maximum starts at -1e30 and only a strictly larger value
+ * replaces it); a row without one gives token 0 and -1e30. Among equal maxima
+ * the lower token id wins (the reference's order depends on its thread
+ * layout). out_max_val may be NULL. Asynchronous; allocates nothing.
+ * OXS_ERR_SHAPE_MISMATCH for vocab 0.
+ */
+int oxs_argmax(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t batch, uint32_t* out_token,
+               float* out_max_val, void* stream);
+
 /* Page-locked host memory that the GPU writes directly (mapped, coherent; the
  * same address on host and device), zeroed. For oxs_decode_io's host fields.
  * OXS_ERR_UNSUPPORTED when the device address would differ from the host's. */

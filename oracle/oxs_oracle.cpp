@@ -560,3 +560,18 @@ void oxo_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, u
     if (!masked) mask[t / 32] |= 1u << (t % 32);
   }
 }
+
+// launch_cuda_argmax (sampling_dfa.cu:2-68): the running maximum starts at
+// -1e30 and only a strictly larger value replaces it; the lower id wins ties.
+void oxo_argmax_floor(const float* row, uint32_t vocab, uint32_t* token, float* value) {
+  float best = -1e30f;
+  uint32_t idx = 0;
+  for (uint32_t i = 0; i < vocab; ++i) {
+    if (row[i] > best) {
+      best = row[i];
+      idx = i;
+    }
+  }
+  *token = idx;
+  *value = best;
+}

@@ -52,6 +52,8 @@ def load() -> ctypes.CDLL:
     lib.oxo_powf.argtypes = [ctypes.c_float, ctypes.c_float]
     lib.oxo_decode_step.restype = ctypes.c_int
     lib.oxo_decode_step.argtypes = [vp, vp, ctypes.c_int]
+    lib.oxo_argmax_floor.restype = None
+    lib.oxo_argmax_floor.argtypes = [vp, ctypes.c_uint32, vp, vp]
     lib.oxo_raw_argmax.restype = ctypes.c_uint32
     lib.oxo_raw_argmax.argtypes = [vp, ctypes.c_uint32]
     lib.oxo_gbnf_mask.restype = None
@@ -233,3 +235,12 @@ def ascii_mask_host(allowed, token_ascii):
     mask = np.zeros(max((vocab + 31) // 32, 1), np.uint32)
     lib.oxo_ascii_mask(_ptr(a), _ptr(ta), vocab, _ptr(mask))
     return mask[: (vocab + 31) // 32]
+
+
+def argmax_floor_host(row):
+    """oxo_argmax_floor: (token, value) of one f32 row."""
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    tok = np.zeros(1, np.uint32)
+    val = np.zeros(1, np.float32)
+    load().oxo_argmax_floor(_ptr(row), row.shape[0], _ptr(tok), _ptr(val))
+    return int(tok[0]), float(val[0])

@@ -1848,6 +1848,50 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   wave_chain<DT>(p, c, row, meff, bf, rs, s_tab);
 }
 
+// ---------------------------------------------------------------- argmax
+
+// launch_cuda_argmax (oxide-backend-cuda/src/kernels/sampling_dfa.cu:2-68,
+// :161-178): per row, the largest logit above -1e30 (its running maximum
+// starts at -1e30 and only a strictly larger value replaces it, so NaN and
+// values <= -1e30 are never taken); a row without one gives token 0 and value
+// -1e30. Among equal maxima the lower token id wins. One 1024-thread block
+// per row, 16-byte loads when the row allows them.
+constexpr int kArgmaxThreads = 1024;
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, uint32_t V,
+                                                               int64_t ld, uint32_t* __restrict__ out_token,
+                                                               float* __restrict__ out_val) {
+  __shared__ uint64_t s_best[kArgmaxThreads / 64];
+  const uint32_t row = blockIdx.x, tid = threadIdx.x;
+  const float* x = logits + (size_t)row * (size_t)ld;
+  const float floor_v = -1e30f;
+  uint64_t best = 0;  // (order key << 32 | ~id), 0 = nothing above the floor
+  auto take = [&](float v, uint32_t i) {
+    if (v > floor_v) {
+      const uint64_t k = ((uint64_t)f2ord(v) << 32) | (uint64_t)(~i);
+      best = k > best ? k : best;
+    }
+  };
+  const bool vec = ((uintptr_t)x % 16 == 0);
+  const uint32_t nv = vec ? V / 4 : 0;
+  for (uint32_t q = tid; q < nv; q += kArgmaxThreads) {
+    const float4 f = *(const float4*)(x + 4 * (size_t)q);
+    take(f.x, 4 * q);
+    take(f.y, 4 * q + 1);
+    take(f.z, 4 * q + 2);
+    take(f.w, 4 * q + 3);
+  }
+  for (uint32_t i = 4 * nv + tid; i < V; i += kArgmaxThreads) take(x[i], i);
+  best = wave_max_u64(best);
+  if ((tid & 63) == 0) s_best[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t b = s_best[0];
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) b = s_best[w] > b ? s_best[w] : b;
+    if (out_token) out_token[row] = b ? ~(uint32_t)b : 0u;
+    if (out_val) out_val[row] = b ? ord2f((uint32_t)(b >> 32)) : floor_v;
+  }
+}
+
 // ---------------------------------------------------------------- host side
 
 struct Geometry {
@@ -2197,6 +2241,16 @@ int oxs_host_alloc(size_t bytes, void** out) {
   memset(h, 0, bytes);
   *out = h;
   return OXS_OK;
+}
+
+int oxs_argmax(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t batch, uint32_t* out_token,
+               float* out_max_val, void* stream) {
+  if (batch == 0) return OXS_OK;
+  if (vocab == 0) return OXS_ERR_SHAPE_MISMATCH;
+  if (!logits || !out_token || logits_ld < (int64_t)vocab) return OXS_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(oxs::argmax_kernel, dim3(batch), dim3(oxs::kArgmaxThreads), 0, (hipStream_t)stream, logits,
+                     vocab, logits_ld, out_token, out_max_val);
+  return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }
 
 int oxs_host_free(void* ptr) {

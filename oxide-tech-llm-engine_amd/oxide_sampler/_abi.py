@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "oxs_sampler_workspace_bytes",
     "oxs_sample_batch",
     "oxs_decode_step",
+    "oxs_argmax",
     "oxs_host_alloc",
     "oxs_host_free",
     "oxs_host_wait",
@@ -209,6 +210,9 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_decode_step.restype = ctypes.c_int
     lib.oxs_decode_step.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.POINTER(OxsDecodeIo),
                                     ctypes.c_void_p]
+    lib.oxs_argmax.restype = ctypes.c_int
+    lib.oxs_argmax.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_void_p,
+                               ctypes.c_void_p, ctypes.c_void_p]
     lib.oxs_host_alloc.restype = ctypes.c_int
     lib.oxs_host_alloc.argtypes = [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]
     lib.oxs_host_free.restype = ctypes.c_int

@@ -408,3 +408,44 @@ def test_host_wait_reads_tagged_slots():
     slots[2] = (0xFFFFFFFF << 32) | 9
     assert lib.oxs_host_wait(ptr(slots), 4, 0, ptr(tokens), 10) == _abi.OXS_ERR_TIMEOUT
     assert lib.oxs_host_wait(None, 4, 0, ptr(tokens), 10) == _abi.OXS_ERR_INVALID_ARGUMENT
+
+
+# ----------------------------------------------------------------------------- the CUDA backend's argmax
+
+def test_oracle_argmax_floor_cases():
+    # launch_cuda_argmax's floor: only values strictly above -1e30 are taken
+    inf, nan = np.inf, np.nan
+    cases = [([1.0, 3.0, 3.0], (1, 3.0)), ([-inf, nan], (0, -1e30)), ([-1e30, -2e30], (0, -1e30)),
+             ([-1e30, -9.9e29], (1, -9.9e29)), ([nan, 2.0, inf, inf], (2, inf)), ([-5.0], (0, -5.0))]
+    for row, (tok, val) in cases:
+        got = oracle.argmax_floor_host(np.array(row, np.float32))
+        assert got[0] == tok and got[1] == np.float32(val), row
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(5000).astype(np.float32)
+    x[[10, 4000]] = 7.0
+    assert oracle.argmax_floor_host(x) == (10, 7.0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,V,ld", [(1, 1, 1), (1, 128256, 128256), (5, 1001, 1003), (64, 32000, 32000),
+                                    (3, 7, 8)])
+def test_gpu_argmax_matches_oracle(torch_gpu, B, V, ld):
+    t = torch_gpu
+    rng = np.random.default_rng(B * V)
+    x = rng.standard_normal((B, ld)).astype(np.float32)
+    x[:, V // 3] = x[:, (2 * V) // 3] = np.float32(9.0)  # ties: the lower id
+    if B > 2:
+        x[1, :] = -np.inf
+        x[2, : V // 2] = np.nan
+        x[2, V // 2:] = np.float32(-2e30)
+    print(f"\n[case] argmax B={B} V={V} ld={ld}", flush=True)
+    d = t.from_numpy(x).to("cuda")
+    tok = t.zeros(B, dtype=t.int32, device="cuda")
+    val = t.zeros(B, dtype=t.float32, device="cuda")
+    lib = _abi.load_library()
+    _abi.check(lib.oxs_argmax(ctypes.c_void_p(d.data_ptr()), V, ld, B, ctypes.c_void_p(tok.data_ptr()),
+                              ctypes.c_void_p(val.data_ptr()), None), "oxs_argmax")
+    t.cuda.synchronize()
+    for b in range(B):
+        want = oracle.argmax_floor_host(x[b, :V])
+        assert int(tok[b]) == want[0] and float(val[b]) == np.float32(want[1]), (b, int(tok[b]), want)
