@@ -199,6 +199,26 @@ def bench_decode(args, torch):
 
     timed(copy_back, 20)
     t_copy = timed(copy_back, n)
+    # the CUDA backend's greedy path (launch_cuda_argmax) as oxs_argmax, 50 calls per graph replay
+    lib = sampler.lib
+    tok = torch.zeros(B, dtype=torch.int32, device=d)
+    val = torch.zeros(B, dtype=torch.float32, device=d)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g_arg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_arg, stream=side):
+        for _ in range(50):
+            lib.oxs_argmax(ctypes.c_void_p(pool[0].data_ptr()), V, V, B, ctypes.c_void_p(tok.data_ptr()),
+                           ctypes.c_void_p(val.data_ptr()), ctypes.c_void_p(side.cuda_stream))
+    g_arg.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        g_arg.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    argmax_us = e0.elapsed_time(e1) * 1e3 / (20 * 50)
     # the reference's hand-off: the whole logits to pinned host memory
     # (oxide-backend-cuda/src/lib.rs:6037-6041), before any CPU sampling
     host = torch.empty(B, V, dtype=torch.float32, pin_memory=True)
@@ -225,6 +245,8 @@ def bench_decode(args, torch):
         "gpu_us_per_step": gpu_us,
         "sample_then_copy_tokens_us": _percentiles(t_copy),
         "reference_logits_to_host_us": _percentiles(t_logits),
+        "greedy_argmax_us": argmax_us,
+        "greedy_argmax_GBps": B * V * 4 / (argmax_us * 1e-6) / 1e9,
         "reference_logits_bytes": B * V * 4,
     }
     if not args.no_cpu:

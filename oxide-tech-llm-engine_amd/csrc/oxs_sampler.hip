@@ -1855,7 +1855,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
 // starts at -1e30 and only a strictly larger value replaces it, so NaN and
 // values <= -1e30 are never taken); a row without one gives token 0 and value
 // -1e30. Among equal maxima the lower token id wins. One 1024-thread block
-// per row, 16-byte loads when the row allows them.
+// per row, eight 16-byte loads in flight per thread when the row allows them.
 constexpr int kArgmaxThreads = 1024;
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, uint32_t V,
                                                                int64_t ld, uint32_t* __restrict__ out_token,
@@ -1873,12 +1873,24 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
   };
   const bool vec = ((uintptr_t)x % 16 == 0);
   const uint32_t nv = vec ? V / 4 : 0;
-  for (uint32_t q = tid; q < nv; q += kArgmaxThreads) {
-    const float4 f = *(const float4*)(x + 4 * (size_t)q);
-    take(f.x, 4 * q);
-    take(f.y, 4 * q + 1);
-    take(f.z, 4 * q + 2);
-    take(f.w, 4 * q + 3);
+  constexpr int kUnroll = 8;  // 16-byte loads in flight per thread
+  for (uint32_t q0 = tid; q0 < nv; q0 += kArgmaxThreads * kUnroll) {
+    float4 f[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t q = q0 + u * kArgmaxThreads;
+      f[u] = *(const float4*)(x + 4 * (size_t)(q < nv ? q : q0));  // repeats of q0 change no maximum
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t q = q0 + u * kArgmaxThreads;
+      if (q < nv) {
+        take(f[u].x, 4 * q);
+        take(f[u].y, 4 * q + 1);
+        take(f[u].z, 4 * q + 2);
+        take(f[u].w, 4 * q + 3);
+      }
+    }
   }
   for (uint32_t i = 4 * nv + tid; i < V; i += kArgmaxThreads) take(x[i], i);
   best = wave_max_u64(best);
