@@ -25,7 +25,8 @@ from .engine import (
     ShapeMismatch,
     configs_to_array,
 )
-from .grammar import DfaSchemaGrammar, GbnfGrammarEngine, GbnfRule, GrammarLogitMasker, SchemaMismatch, TokenBytes
+from .grammar import (DfaSchemaGrammar, GbnfGrammarEngine, GbnfRule, GrammarConstraintType, GrammarLogitMasker,
+                      SchemaMismatch, StructuredOutputEngine, TokenBytes)
 from .decode import DecodeLoop, TokenEvent
 from ._abi import (
     LibraryMissing,
@@ -45,6 +46,8 @@ __all__ = [
     "GbnfGrammarEngine",
     "GbnfRule",
     "GrammarLogitMasker",
+    "GrammarConstraintType",
+    "StructuredOutputEngine",
     "SchemaMismatch",
     "TokenBytes",
     "DecodeLoop",

@@ -353,3 +353,43 @@ class GrammarLogitMasker:
             return
         n = min(len(vocab_ascii_bytes), len(logits))
         _mask_in_place(logits, self.token_mask(list(vocab_ascii_bytes)[:n]), n)
+
+
+class GrammarConstraintType:
+    """GrammarConstraintType (crates/oxide-server/src/grammar_engine.rs:10-15)."""
+
+    def __init__(self, kind: str, text: str):
+        if kind not in ("JsonSchema", "Regex", "Ebnf"):
+            raise ValueError(f"unknown constraint type {kind}")
+        self.kind, self.text = kind, text
+
+    @classmethod
+    def JsonSchema(cls, schema: str) -> "GrammarConstraintType":
+        return cls("JsonSchema", schema)
+
+    @classmethod
+    def Regex(cls, pattern: str) -> "GrammarConstraintType":
+        return cls("Regex", pattern)
+
+    @classmethod
+    def Ebnf(cls, rules: str) -> "GrammarConstraintType":
+        return cls("Ebnf", rules)
+
+
+class StructuredOutputEngine:
+    """StructuredOutputEngine (grammar_engine.rs:17-75): every constraint type
+    compiles to DfaSchemaGrammar::new_simple_json_validator (:26-38, :67-75);
+    compute_token_mask runs on the GPU (oxs_dfa_mask)."""
+
+    def __init__(self, grammar: DfaSchemaGrammar):
+        self.grammar = grammar
+
+    @classmethod
+    def compile(cls, constraint: GrammarConstraintType) -> "StructuredOutputEngine":
+        return cls(DfaSchemaGrammar.new_simple_json_validator())
+
+    def compute_token_mask(self, current_state: int, vocab) -> List[bool]:
+        """grammar_engine.rs:40-65: True where the token's bytes walk from current_state."""
+        tb = vocab if isinstance(vocab, TokenBytes) else TokenBytes([bytes(v) for v in vocab])
+        words = self.grammar.token_masks(tb, [current_state])[0].cpu().numpy().view(np.uint32)
+        return np.unpackbits(words.view(np.uint8), bitorder="little")[: tb.vocab].astype(bool).tolist()

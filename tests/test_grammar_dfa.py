@@ -243,3 +243,20 @@ def test_gpu_state_mask_gather_matches_direct_walk(torch_gpu, n, V):
         direct = g.token_masks(tb, states).cpu().numpy().view(np.uint32)
         np.testing.assert_array_equal(got, direct)
         np.testing.assert_array_equal(got, oracle.dfa_mask_host(table, n, off, by, states))
+
+
+@pytest.mark.gpu
+def test_gpu_structured_output_engine_token_mask(torch_gpu):
+    # grammar_engine.rs:40-65: every constraint type falls back to the JSON validator (:67-75)
+    from oxide_sampler.grammar import GrammarConstraintType, StructuredOutputEngine
+    vocab = [b'{"', b"123", b"hello", b"", b"{", b'{"a":1}', b"}"]
+    for c in (GrammarConstraintType.JsonSchema("{}"), GrammarConstraintType.Regex(".*"),
+              GrammarConstraintType.Ebnf("root ::= x")):
+        eng = StructuredOutputEngine.compile(c)
+        assert eng.compute_token_mask(0, vocab) == [True, False, False, True, True, True, False]
+        off, by = pack(vocab)
+        for state in (0, 1, 4, 5, 9):
+            want = oracle.dfa_mask_host(eng.grammar.transitions, eng.grammar.num_states, off, by,
+                                        np.array([state], np.uint32))
+            assert eng.compute_token_mask(state, vocab) == [bool((want[0, t // 32] >> (t % 32)) & 1)
+                                                            for t in range(len(vocab))]
