@@ -372,6 +372,46 @@ int oxs_gbnf_mask(const oxs_gbnf_rule* rule, const oxs_token_bytes* tokens, uint
 int oxs_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, uint32_t vocab, uint32_t* mask,
                    void* stream);
 
+/*
+ * LM head: the projection that produces the logits the sampler reads, in the
+ * reference's GGUF Q8_0 format (oxide-backend-cuda/src/lib.rs:4013-4035, the
+ * batched decode; :3229-3243 for the last prompt token).
+ *
+ * q8_1 activations: n / 32 blocks of 36 bytes, {f16 d, f16 sum, int8 qs[32]}
+ * (common_types.cuh:8-11). Q8_0 weights: m rows (tokens) of k / 32 blocks of
+ * 34 bytes, {f16 d, int8 qs[32]} (common_types.cuh:13-16).
+ */
+
+/* launch_cuda_quantize_q8_1 (kernels/launch_wrappers.cu:143-154,
+ * quantize_f32_to_q8_1_cuda_kernel norms_rope.cu:2-29): each 32-value block of
+ * x becomes d = amax / 127, qs = roundf(x / d) (x * (1 / d), 0 when d == 0),
+ * sum = the 32 values summed in the kernel's butterfly order. n / 32 blocks
+ * are written (a remainder is ignored, as there); n == 0 does nothing. */
+int oxs_quantize_q8_1(const float* x, uint32_t n, void* y_q8_1, void* stream);
+
+/* Bytes of the packed weight layout oxs_mmvq_q8_0 reads for an m x k Q8_0
+ * matrix: per 32 tokens and per 32-wide block of k, 1024 bytes of quants in
+ * the order the matrix cores take them and 64 bytes of scales (1088 bytes;
+ * tokens past m are zero). 0 when k is not a multiple of 128. */
+size_t oxs_q8_0_packed_bytes(uint32_t m, uint32_t k);
+
+/* Repacks GGUF Q8_0 rows (w, [m][k / 32] 34-byte blocks) into the packed
+ * layout, once at model load. k must be a multiple of 128
+ * (OXS_ERR_UNSUPPORTED otherwise). No counterpart in the reference, whose
+ * kernel reads the GGUF blocks directly. */
+int oxs_pack_q8_0(const void* w, uint32_t m, uint32_t k, void* w_packed, void* stream);
+
+/* launch_cuda_mmvq_q8_0 (kernels/launch_wrappers.cu:156-200,
+ * mmvq_q8_0_cuda_kernel quant_gemv_standard.cu:418-513): y[c][t] for batch
+ * column c < batch and token t < m, from the packed weights and the q8_1
+ * activations x ([batch][k / 32] blocks). Each value is the reference's, bit
+ * for bit: per block b the exact integer dot of the 32 quants, accumulated as
+ * A[b % 4] = fmaf(d_w * d_x, (float)dot, A[b % 4]) in increasing b, then
+ * (A0 + A2) + (A1 + A3). m == 0 or batch == 0 does nothing; k must be a
+ * multiple of 128. */
+int oxs_mmvq_q8_0(float* y, const void* w_packed, const void* x_q8_1, uint32_t m, uint32_t k, uint32_t batch,
+                  void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

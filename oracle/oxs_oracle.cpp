@@ -575,3 +575,102 @@ void oxo_argmax_floor(const float* row, uint32_t vocab, uint32_t* token, float* 
   *token = idx;
   *value = best;
 }
+
+// ---------------------------------------------------------------- LM head (Q8_0 x q8_1)
+
+// IEEE binary16 <-> binary32: the conversions behind __half2float and
+// __float2half (round to nearest, ties to even), written from the formats.
+float oxo_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0) {
+    const float v = (float)mant * (1.0f / 16777216.0f);  // mant * 2^-24, exact
+    memcpy(&bits, &v, 4);
+    bits |= sign;
+  } else if (e == 31) {
+    bits = sign | 0x7f800000u | (mant << 13);
+  } else {
+    bits = sign | ((e - 15u + 127u) << 23) | (mant << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t oxo_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));  // NaN stays NaN
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);                         // >= 65520: infinity
+  if (ax < 0x38800000u) {  // below 2^-14: a subnormal half, round(|f| * 2^24)
+    float a;
+    memcpy(&a, &ax, 4);
+    return (uint16_t)(sign | (uint32_t)nearbyintf(a * 16777216.0f));
+  }
+  uint32_t h = ((((ax >> 23) - 127u + 15u)) << 10) | ((ax >> 13) & 0x3ffu);
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;  // a carry moves into the exponent
+  return (uint16_t)(sign | h);
+}
+
+// quantize_f32_to_q8_1_cuda_kernel (norms_rope.cu:2-29): one 32-lane group per
+// block; amax and sum by an xor butterfly over offsets 16, 8, 4, 2, 1 (lane 0's
+// sum is stored); d = amax / 127, id = 1 / d (0 when d == 0),
+// q = (int8) roundf(x * id); ds = (half d, half sum).
+void oxo_quantize_q8_1(const float* x, uint32_t n, uint8_t* y) {
+  for (uint32_t blk = 0; blk < n / 32; ++blk) {
+    const float* v = x + (size_t)blk * 32;
+    float a[32], s[32];
+    for (int i = 0; i < 32; ++i) {
+      a[i] = fabsf(v[i]);
+      s[i] = v[i];
+    }
+    for (int o = 16; o > 0; o >>= 1) {
+      float a2[32], s2[32];
+      for (int i = 0; i < 32; ++i) {
+        a2[i] = fmaxf(a[i], a[i ^ o]);
+        s2[i] = s[i] + s[i ^ o];
+      }
+      memcpy(a, a2, sizeof a);
+      memcpy(s, s2, sizeof s);
+    }
+    const float d = a[0] / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    uint8_t* out = y + (size_t)blk * 36;
+    const uint16_t hd = oxo_f32_to_f16(d), hs = oxo_f32_to_f16(s[0]);
+    memcpy(out, &hd, 2);
+    memcpy(out + 2, &hs, 2);
+    for (int i = 0; i < 32; ++i) out[4 + i] = (uint8_t)(int8_t)roundf(v[i] * id);
+  }
+}
+
+// mmvq_q8_0_cuda_kernel (quant_gemv_standard.cu:425-513), per (column c,
+// token t): the lanes with sub_idx 0 of block_in_warp j = 0..3 accumulate the
+// blocks b = j, j + 4, ... in increasing b as
+// thread_dot += (d * d8) * (float)dot_int, which nvcc's default contraction
+// (-fmad=true; build.rs passes only -O3) makes fmaf(d * d8, dot, thread_dot);
+// dot_int is the exact integer dot of the 32 quants (dp4a and an integer
+// butterfly). Then two shuffles down add lane 16 into lane 0 and lane 24 into
+// lane 8, then lane 8 into lane 0: (A0 + A2) + (A1 + A3).
+void oxo_mmvq_q8_0(float* y, const uint8_t* w, const uint8_t* x, uint32_t m, uint32_t k, uint32_t batch) {
+  const uint32_t nb = k / 32;
+  for (uint32_t c = 0; c < batch; ++c) {
+    for (uint32_t t = 0; t < m; ++t) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t* wb = w + ((size_t)t * nb + b) * 34;
+        const uint8_t* xb = x + ((size_t)c * nb + b) * 36;
+        int dot = 0;
+        for (int e = 0; e < 32; ++e) dot += (int)(int8_t)wb[2 + e] * (int)(int8_t)xb[4 + e];
+        uint16_t hw, hx;
+        memcpy(&hw, wb, 2);
+        memcpy(&hx, xb, 2);
+        const float dd = oxo_f16_to_f32(hw) * oxo_f16_to_f32(hx);
+        acc[b % 4] = fmaf(dd, (float)dot, acc[b % 4]);
+      }
+      y[(size_t)c * m + t] = (acc[0] + acc[2]) + (acc[1] + acc[3]);
+    }
+  }
+}

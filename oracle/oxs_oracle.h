@@ -108,6 +108,15 @@ float oxo_logf(float x);
 float oxo_log2f(float x);
 float oxo_powf(float x, float y);
 
+/* LM head (Q8_0 weights x q8_1 activations), the reference CUDA backend's
+ * formats: IEEE half conversions, launch_cuda_quantize_q8_1
+ * (norms_rope.cu:2-29) and launch_cuda_mmvq_q8_0 (quant_gemv_standard.cu:425-513)
+ * on the GGUF layout ([m][k / 32] 34-byte blocks; y is [batch][m]). */
+float oxo_f16_to_f32(uint16_t h);
+uint16_t oxo_f32_to_f16(float f);
+void oxo_quantize_q8_1(const float* x, uint32_t n, uint8_t* y);
+void oxo_mmvq_q8_0(float* y, const uint8_t* w, const uint8_t* x, uint32_t m, uint32_t k, uint32_t batch);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,12 @@ def load() -> ctypes.CDLL:
                                   ctypes.c_uint32, vp]
     lib.oxo_ascii_mask.restype = None
     lib.oxo_ascii_mask.argtypes = [vp, vp, ctypes.c_uint32, vp]
+    lib.oxo_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.oxo_f16_to_f32.restype = ctypes.c_float
+    lib.oxo_f32_to_f16.argtypes = [ctypes.c_float]
+    lib.oxo_f32_to_f16.restype = ctypes.c_uint16
+    lib.oxo_quantize_q8_1.argtypes = [vp, ctypes.c_uint32, vp]
+    lib.oxo_mmvq_q8_0.argtypes = [vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
     lib.oxo_dfa_mask.restype = None
     lib.oxo_dfa_mask.argtypes = [vp, ctypes.c_uint32, vp, vp, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32,
                                  vp, ctypes.c_int64]
@@ -244,3 +250,31 @@ def argmax_floor_host(row):
     val = np.zeros(1, np.float32)
     load().oxo_argmax_floor(_ptr(row), row.shape[0], _ptr(tok), _ptr(val))
     return int(tok[0]), float(val[0])
+
+
+def f16_to_f32_host(h):
+    lib = load()
+    return np.array([lib.oxo_f16_to_f32(int(v)) for v in np.asarray(h, np.uint16).ravel()], np.float32)
+
+
+def f32_to_f16_host(f):
+    lib = load()
+    return np.array([lib.oxo_f32_to_f16(float(v)) for v in np.asarray(f, np.float32).ravel()], np.uint16)
+
+
+def quantize_q8_1_host(x):
+    """oxo_quantize_q8_1: float32 [..., n] -> uint8 [n / 32 blocks x 36 bytes] (flattened input)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros((x.size // 32) * 36, np.uint8)
+    load().oxo_quantize_q8_1(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def mmvq_q8_0_host(w, x_q8_1, m, k, batch):
+    """oxo_mmvq_q8_0: GGUF Q8_0 bytes [m][k / 32][34] and q8_1 bytes [batch][k / 32][36] -> y [batch, m]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x_q8_1, dtype=np.uint8)
+    assert w.size == m * (k // 32) * 34 and x.size == batch * (k // 32) * 36
+    y = np.zeros((batch, m), np.float32)
+    load().oxo_mmvq_q8_0(_ptr(y), _ptr(w), _ptr(x), m, k, batch)
+    return y

@@ -1,0 +1,225 @@
+// oxs_lm_head.hip — the LM head that feeds the sampler, in the reference CUDA
+// backend's GGUF formats (Q8_0 weights x q8_1 activations), on gfx950.
+//
+// The reference's batched decode quantizes the final hidden states to q8_1
+// and projects them with launch_cuda_mmvq_q8_0
+// (oxide-backend-cuda/src/lib.rs:4013-4035). Here:
+// - quantize_q8_1_kernel: one 32-lane group per q8_1 block, amax and sum by
+//   the same xor butterfly, so the stored sum is the reference's bit for bit;
+// - pack_q8_0_kernel: a one-time repack of the GGUF rows into tiles of 32
+//   tokens x one 32-wide k block, with the quants in the order the matrix
+//   cores read them (one 16-byte load per lane per block) and the 32 scales
+//   permuted to the rows each lane's accumulators hold;
+// - mmvq_q8_0_kernel: per wavefront 32 tokens x 64 batch columns. Each k block
+//   is two v_mfma_i32_32x32x32_i8, giving the exact integer dot of every
+//   (token, column) pair; the float accumulation then follows the reference
+//   kernel exactly (four accumulators by b % 4, fmaf(d_w * d_x, dot, acc),
+//   then (A0 + A2) + (A1 + A3)), so y is the reference's to the last bit.
+//
+// Bound: HBM (34 bytes per 32 weights, read once; activations and y are small
+// beside them) and, at 64 columns, the VALU's three operations per
+// (token, column, block) that the reference's float order needs.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/oxide_sampler.h"
+
+namespace oxs_lm {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kQ81Bytes = 36;       // {f16 d, f16 sum, int8 qs[32]} (common_types.cuh:8-11)
+constexpr int kQ80Bytes = 34;       // {f16 d, int8 qs[32]} (common_types.cuh:13-16)
+constexpr int kPackedBlock = 1088;  // 32 tokens x one k block: 64 lanes x 16 quant bytes, then 32 f16 scales
+constexpr int kColsPerBlock = 64;   // batch columns per workgroup: two 32-column MFMA tiles
+constexpr int kGroupsPerBlock = 4;  // token groups (wavefronts) per workgroup
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float half_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t float_to_half(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Row i of the 32 x 32 MFMA output held in register r of a lane in half g
+// (lanes 32g .. 32g + 31): 8 (r / 4) + 4 g + r % 4.
+__device__ __forceinline__ uint32_t out_row(uint32_t r, uint32_t g) { return 8u * (r >> 2) + 4u * g + (r & 3u); }
+
+// quantize_f32_to_q8_1_cuda_kernel (norms_rope.cu:2-29): eight 32-lane groups
+// per workgroup, one q8_1 block each.
+__global__ __launch_bounds__(kThreads) void quantize_q8_1_kernel(const float* __restrict__ x, uint32_t nblocks,
+                                                                 uint8_t* __restrict__ y) {
+  const uint32_t lane = threadIdx.x & 31u;
+  const uint32_t blk = blockIdx.x * (kThreads / 32) + (threadIdx.x >> 5);
+  if (blk >= nblocks) return;  // the whole 32-lane group leaves together
+  const float v = x[(size_t)blk * 32 + lane];
+  float amax = fabsf(v), sum = v;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+    sum += __shfl_xor(sum, o, 32);
+  }
+  const float d = amax / 127.0f;
+  const float id = d > 0.0f ? 1.0f / d : 0.0f;
+  uint8_t* out = y + (size_t)blk * kQ81Bytes;
+  out[4 + lane] = (uint8_t)(int8_t)roundf(v * id);
+  if (lane == 0) {
+    *(uint16_t*)out = float_to_half(d);
+    *(uint16_t*)(out + 2) = float_to_half(sum);
+  }
+}
+
+// One wavefront per (token group, k block): lane l writes quant bytes
+// [16 (l / 32), +16) of token 32 tg + l % 32 at offset 16 l; lanes 0..31 write
+// the scales, position p holding token out_row(p % 16, p / 16). Tokens past m
+// are zero.
+__global__ __launch_bounds__(kThreads) void pack_q8_0_kernel(const uint8_t* __restrict__ w, uint32_t m, uint32_t nb,
+                                                             uint64_t pieces, uint8_t* __restrict__ out) {
+  const uint64_t gid = (uint64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (gid >= pieces) return;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t tg = (uint32_t)(gid / nb), b = (uint32_t)(gid % nb);
+  uint8_t* dst = out + gid * kPackedBlock;
+  {
+    const uint32_t t = tg * 32u + (lane & 31u), g = lane >> 5;
+    uint32_t q[4] = {0u, 0u, 0u, 0u};
+    if (t < m) {
+      const uint8_t* src = w + ((size_t)t * nb + b) * kQ80Bytes + 2 + 16 * g;  // 2-byte aligned
+#pragma unroll
+      for (int i = 0; i < 16; ++i) q[i / 4] |= (uint32_t)src[i] << (8 * (i % 4));
+    }
+    *(uint4*)(dst + 16 * lane) = make_uint4(q[0], q[1], q[2], q[3]);
+  }
+  if (lane < 32) {
+    const uint32_t t = tg * 32u + out_row(lane & 15u, lane >> 4);
+    uint16_t s = 0;
+    if (t < m) {
+      const uint8_t* src = w + ((size_t)t * nb + b) * kQ80Bytes;
+      s = (uint16_t)(src[0] | (src[1] << 8));
+    }
+    *(uint16_t*)(dst + 1024 + 2 * lane) = s;
+  }
+}
+
+// mmvq_q8_0_cuda_kernel (quant_gemv_standard.cu:425-513) for 64 columns x 128
+// tokens per workgroup; each wavefront owns one group of 32 tokens and both
+// column tiles. No block barriers: wavefronts past the last group return.
+__global__ __launch_bounds__(kThreads) void mmvq_q8_0_kernel(float* __restrict__ y, const uint8_t* __restrict__ wp,
+                                                             const uint8_t* __restrict__ x, uint32_t m, uint32_t nb,
+                                                             uint32_t batch) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t tg = blockIdx.x * kGroupsPerBlock + wave;
+  if (tg >= (m + 31u) / 32u) return;
+  const uint32_t g = lane >> 5, j = lane & 31u;
+  const uint32_t c0 = blockIdx.y * kColsPerBlock;
+  // this lane's B-operand columns, clamped into the batch (their results are not stored)
+  const uint32_t colA = min(c0 + j, batch - 1u), colB = min(c0 + 32u + j, batch - 1u);
+  const uint8_t* xa = x + (size_t)colA * nb * kQ81Bytes;
+  const uint8_t* xb = x + (size_t)colB * nb * kQ81Bytes;
+  const uint8_t* wg = wp + (size_t)tg * nb * kPackedBlock;
+
+  float acc[2][4][16];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][q][r] = 0.0f;
+  const v16i zero = {};
+
+  for (uint32_t b0 = 0; b0 < nb; b0 += 4) {  // nb is a multiple of 4
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // block b0 + q goes to accumulator q = b % 4
+      const uint8_t* blk = wg + (size_t)(b0 + q) * kPackedBlock;
+      const v4i a = *(const v4i*)(blk + 16 * lane);
+      const uint4 s0 = *(const uint4*)(blk + 1024 + 32 * g);
+      const uint4 s1 = *(const uint4*)(blk + 1024 + 32 * g + 16);
+      const uint32_t* pa = (const uint32_t*)(xa + (size_t)(b0 + q) * kQ81Bytes);  // 4-byte aligned
+      const uint32_t* pb = (const uint32_t*)(xb + (size_t)(b0 + q) * kQ81Bytes);
+      const v4i ba = {(int)pa[1 + 4 * g], (int)pa[2 + 4 * g], (int)pa[3 + 4 * g], (int)pa[4 + 4 * g]};
+      const v4i bb = {(int)pb[1 + 4 * g], (int)pb[2 + 4 * g], (int)pb[3 + 4 * g], (int)pb[4 + 4 * g]};
+      const float dxa = half_to_float((uint16_t)(pa[0] & 0xffffu));
+      const float dxb = half_to_float((uint16_t)(pb[0] & 0xffffu));
+      const v16i da = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, ba, zero, 0, 0, 0);
+      const v16i db = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bb, zero, 0, 0, 0);
+      const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float dw = half_to_float((uint16_t)(sw[r / 2] >> (16 * (r % 2))));
+        acc[0][q][r] = __builtin_fmaf(dw * dxa, (float)da[r], acc[0][q][r]);
+        acc[1][q][r] = __builtin_fmaf(dw * dxb, (float)db[r], acc[1][q][r]);
+      }
+    }
+  }
+
+  // (A0 + A2) + (A1 + A3); registers 4 q' .. 4 q' + 3 hold four consecutive tokens
+  const bool vec = (m & 3u) == 0u;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t col = c0 + 32u * t + j;
+    if (col >= batch) continue;
+    float* yrow = y + (size_t)col * m;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * qq + e;
+        v[e] = (acc[t][0][r] + acc[t][2][r]) + (acc[t][1][r] + acc[t][3][r]);
+      }
+      const uint32_t tok = tg * 32u + out_row(4u * qq, g);
+      if (vec && tok + 3u < m) {
+        *(float4*)(yrow + tok) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (tok + e < m) yrow[tok + e] = v[e];
+      }
+    }
+  }
+}
+
+}  // namespace oxs_lm
+
+static int launch_status() { return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP; }
+
+extern "C" int oxs_quantize_q8_1(const float* x, uint32_t n, void* y_q8_1, void* stream) {
+  const uint32_t nblocks = n / 32u;
+  if (nblocks == 0) return OXS_OK;
+  if (!x || !y_q8_1) return OXS_ERR_INVALID_ARGUMENT;
+  const uint32_t per = oxs_lm::kThreads / 32;
+  hipLaunchKernelGGL(oxs_lm::quantize_q8_1_kernel, dim3((nblocks + per - 1) / per), dim3(oxs_lm::kThreads), 0,
+                     (hipStream_t)stream, x, nblocks, (uint8_t*)y_q8_1);
+  return launch_status();
+}
+
+extern "C" size_t oxs_q8_0_packed_bytes(uint32_t m, uint32_t k) {
+  if (k == 0 || k % 128u != 0) return 0;
+  return (size_t)((m + 31u) / 32u) * (k / 32u) * oxs_lm::kPackedBlock;
+}
+
+extern "C" int oxs_pack_q8_0(const void* w, uint32_t m, uint32_t k, void* w_packed, void* stream) {
+  if (k == 0 || k % 128u != 0) return OXS_ERR_UNSUPPORTED;
+  if (m == 0) return OXS_OK;
+  if (!w || !w_packed) return OXS_ERR_INVALID_ARGUMENT;
+  const uint32_t nb = k / 32u;
+  const uint64_t pieces = (uint64_t)((m + 31u) / 32u) * nb;
+  const uint64_t per = oxs_lm::kThreads / 64;
+  const uint64_t grid = (pieces + per - 1) / per;
+  if (grid > 0x7fffffffull) return OXS_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(oxs_lm::pack_q8_0_kernel, dim3((uint32_t)grid), dim3(oxs_lm::kThreads), 0, (hipStream_t)stream,
+                     (const uint8_t*)w, m, nb, pieces, (uint8_t*)w_packed);
+  return launch_status();
+}
+
+extern "C" int oxs_mmvq_q8_0(float* y, const void* w_packed, const void* x_q8_1, uint32_t m, uint32_t k,
+                             uint32_t batch, void* stream) {
+  if (m == 0 || k == 0 || batch == 0) return OXS_OK;  // as launch_cuda_mmvq_q8_0's early return
+  if (k % 128u != 0) return OXS_ERR_UNSUPPORTED;
+  if (!y || !w_packed || !x_q8_1) return OXS_ERR_INVALID_ARGUMENT;
+  const uint32_t groups = (m + 31u) / 32u;
+  const dim3 grid((groups + oxs_lm::kGroupsPerBlock - 1) / oxs_lm::kGroupsPerBlock,
+                  (batch + oxs_lm::kColsPerBlock - 1) / oxs_lm::kColsPerBlock);
+  if (grid.y > 65535u) return OXS_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(oxs_lm::mmvq_q8_0_kernel, grid, dim3(oxs_lm::kThreads), 0, (hipStream_t)stream, y,
+                     (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, k / 32u, batch);
+  return launch_status();
+}

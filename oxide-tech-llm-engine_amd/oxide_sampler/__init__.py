@@ -28,6 +28,7 @@ from .engine import (
 from .grammar import (DfaSchemaGrammar, GbnfGrammarEngine, GbnfRule, GrammarConstraintType, GrammarLogitMasker,
                       SchemaMismatch, StructuredOutputEngine, TokenBytes)
 from .decode import DecodeLoop, TokenEvent
+from .lm_head import LmHeadQ8_0, quantize_q8_1
 from ._abi import (
     LibraryMissing,
     OxsError,
@@ -52,6 +53,8 @@ __all__ = [
     "TokenBytes",
     "DecodeLoop",
     "TokenEvent",
+    "LmHeadQ8_0",
+    "quantize_q8_1",
     "LibraryMissing",
     "OxsError",
     "load_library",

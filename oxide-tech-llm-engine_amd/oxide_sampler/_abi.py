@@ -59,6 +59,10 @@ EXPORTED_SYMBOLS = (
     "oxs_dfa_mask_gather",
     "oxs_gbnf_mask",
     "oxs_ascii_mask",
+    "oxs_quantize_q8_1",
+    "oxs_q8_0_packed_bytes",
+    "oxs_pack_q8_0",
+    "oxs_mmvq_q8_0",
 )
 
 OXS_DFA_ERROR_STATE = 0xFFFFFFFF
@@ -233,6 +237,15 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_ascii_mask.restype = ctypes.c_int
     lib.oxs_ascii_mask.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
                                    ctypes.c_void_p]
+    lib.oxs_quantize_q8_1.restype = ctypes.c_int
+    lib.oxs_quantize_q8_1.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.oxs_q8_0_packed_bytes.restype = ctypes.c_size_t
+    lib.oxs_q8_0_packed_bytes.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    lib.oxs_pack_q8_0.restype = ctypes.c_int
+    lib.oxs_pack_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.oxs_mmvq_q8_0.restype = ctypes.c_int
+    lib.oxs_mmvq_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                  ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
     if lib.oxs_abi_version() != OXS_ABI_VERSION:
         raise RuntimeError(f"liboxide_sampler ABI {lib.oxs_abi_version()} != {OXS_ABI_VERSION}")
     if path is None:
