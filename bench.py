@@ -22,7 +22,10 @@ Two secondary measurements print their own JSON line instead:
                        device-to-host copy of the tokens and the reference's
                        copy of the whole logits to the host;
   --workload dfa_mask  grammar masks (oxs_dfa_mask) for 128 rows over a
-                       128256-token vocabulary.
+                       128256-token vocabulary;
+  --workload lm_head   the Q8_0 LM head that produces the logits (64 columns x
+                       128256 tokens x hidden 4096), and the chain quantize ->
+                       LM head -> sampler of one decode step.
 """
 from __future__ import annotations
 
@@ -352,6 +355,124 @@ def bench_dfa_mask(args, torch):
     print(json.dumps(result), flush=True)
 
 
+def bench_lm_head(args, torch):
+    """The Q8_0 LM head of the batched decode (oxs_quantize_q8_1 + oxs_mmvq_q8_0)
+    at config 2's shape: 64 columns x 128256 tokens x hidden 4096, then the
+    chain quantize -> LM head -> oxs_sample_batch that one decode step runs."""
+    from oxide_sampler import BatchSampler, LmHeadQ8_0, _abi, quantize_q8_1  # noqa: PLC0415
+    from oxide_sampler import workloads as wl  # noqa: PLC0415
+
+    m, k, B = 128256, 4096, 64
+    nb = k // 32
+    rng = np.random.default_rng(0x5EED0011)
+    blocks = np.empty((m, nb, 34), np.uint8)
+    blocks[:, :, 2:] = rng.integers(-128, 128, size=(m, nb, 32), dtype=np.int8).view(np.uint8)
+    blocks[:, :, 0:2] = rng.uniform(0.002, 0.05, size=(m, nb)).astype(np.float16).view(np.uint8).reshape(m, nb, 2)
+    w_host = blocks.reshape(-1)
+    del blocks
+    head = LmHeadQ8_0(w_host, m, k)
+    x = torch.from_numpy(rng.normal(0, 1.5, size=(B, k)).astype(np.float32)).cuda()
+    xq = quantize_q8_1(x).view(B, -1)
+    y = torch.empty(B, m, dtype=torch.float32, device="cuda")
+    head.project(xq, out=y)
+    torch.cuda.synchronize()
+    y_eager = y.clone()
+
+    # the decode step's sampler on these logits: config 2's chain and history
+    w = wl.config2(batch=B, vocab=m)
+    sampler = BatchSampler(B, m, 256)
+    cfg, _, _, _ = w.packed_configs()
+    d_cfg = torch.from_numpy(cfg).cuda()
+    d_hist = torch.from_numpy(w.history.view(np.int32).copy()).cuda()
+    d_hlen = torch.from_numpy(w.history_len.view(np.int32).copy()).cuda()
+    d_u = torch.from_numpy(w.uniforms).cuda()
+    tokens = torch.empty(B, dtype=torch.int32, device="cuda")
+    status = torch.empty(B, dtype=torch.int32, device="cuda")
+    b = _abi.OxsBatch()
+    b.batch, b.vocab, b.logits_dtype, b.flags = B, m, _abi.OXS_DTYPE_F32, 0
+    b.logits_ld, b.logits, b.configs = m, y.data_ptr(), d_cfg.data_ptr()
+    b.history, b.history_ld, b.history_len = d_hist.data_ptr(), d_hist.stride(0), d_hlen.data_ptr()
+    b.uniforms, b.out_tokens, b.out_status = d_u.data_ptr(), tokens.data_ptr(), status.data_ptr()
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    reps = 10
+    g_head, g_chain = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_head, stream=stream):
+        for _ in range(reps):
+            head.project(xq, out=y)
+    with torch.cuda.graph(g_chain, stream=stream):
+        for _ in range(reps):
+            quantize_q8_1(x, out=xq, stream=stream)
+            head.project(xq, out=y, stream=stream)
+            sampler.launch(b, stream)
+    torch.cuda.synchronize()
+
+    def timed(graph, n):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+        with torch.cuda.stream(stream):
+            evs[0].record(stream)
+            for i in range(n):
+                graph.replay()
+                evs[i + 1].record(stream)
+        torch.cuda.synchronize()
+        return [evs[i].elapsed_time(evs[i + 1]) * 1e3 / reps for i in range(n)]
+
+    n = max(5, args.steps // 400)
+    timed(g_head, 3)
+    head_us = timed(g_head, n)
+    assert torch.equal(y, y_eager), "graph replay of the LM head differs from the eager launch"
+    timed(g_chain, 3)
+    chain_us = timed(g_chain, n)
+    assert (status == 0).all().item(), "sampler reported a non-OK row status"
+    med = float(np.median(head_us))
+    alg = m * nb * 34 + B * nb * 36 + B * m * 4
+    achieved = alg / (med * 1e-6) / 1e9
+    result = {
+        "metric": "Q8_0 LM head logits/s (batch 64 x vocab 128256 x hidden 4096), bit-exact with launch_cuda_mmvq_q8_0",
+        "value": B * m / (med * 1e-6),
+        "unit": "logits/s",
+        "higher_is_better": True,
+        "n_gpus": 1,
+        "steps": n * reps,
+        "median_us_per_step": med,
+        "dtype": "int8 x int8 -> i32 (MFMA), f32 accumulation in the reference's order",
+        "data": "synthetic Q8_0 weights (uniform int8 quants, f16 scales in [0.002, 0.05]), hidden ~ N(0, 1.5)",
+        "config": {"workload": "lm_head: oxs_mmvq_q8_0, m=128256, k=4096, batch=64 (config 2's decode batch); "
+                               "chain = oxs_quantize_q8_1 + oxs_mmvq_q8_0 + oxs_sample_batch (config-2 chain)",
+                   "m": m, "k": k, "batch": B, "launch": "hip_graph"},
+        "chain_us_per_step": float(np.median(chain_us)),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": alg,
+                     "kernel": "mmvq_q8_0_kernel",
+                     "note": "VALU-bound: the reference's float order costs 64 VALU instructions per "
+                             "(32 tokens x 32 columns x k block) beside one MFMA"},
+    }
+    tpath = ROOT / "profiles" / "lm_head_pmc_traffic.json"
+    if tpath.exists():
+        t = json.loads(tpath.read_text())
+        result["roofline"]["traffic"] = t["traffic_bytes_per_launch"]
+        result["roofline"]["traffic_source"] = str(tpath.relative_to(ROOT))
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oxs_oracle_ctypes as oracle  # noqa: PLC0415 — baseline leg only
+
+        rows = 512  # a bounded sample: 512 token rows x all 64 columns
+        sub = w_host[: rows * nb * 34]
+        xq_host = oracle.quantize_q8_1_host(x.cpu().numpy())
+        t0 = time.perf_counter()
+        done = 0
+        while time.perf_counter() - t0 < args.cpu_seconds or done == 0:
+            want = oracle.mmvq_q8_0_host(sub, xq_host, rows, k, B)
+            done += 1
+        dt = time.perf_counter() - t0
+        assert np.array_equal(want.view(np.uint32), y_eager[:, :rows].cpu().numpy().view(np.uint32)), \
+            "the GPU logits differ from the oracle's"
+        result["cpu_baseline"] = {"value": done * rows * B / dt, "unit": "logits/s", "cores": 1, "kind": "port",
+                                  "sample": f"{done} passes of the first {rows} tokens x 64 columns"}
+    print(json.dumps(result), flush=True)
+
+
 def read_traffic(path):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
     try:
@@ -449,8 +570,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only 8 plain 256 MiB device copies (scale for the rocprofv3 byte counters)")
     ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
-    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask"), default="sample",
-                    help="sample: the headline config-2 line; decode / dfa_mask: secondary measurements")
+    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head"), default="sample",
+                    help="sample: the headline config-2 line; decode / dfa_mask / lm_head: secondary measurements")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="turn four rocprofv3 --pmc output folders into the traffic summary and exit")
     ap.add_argument("--trace-summary", default=str(ROOT / "profiles" / "config2_kernel_trace.json"))
@@ -487,6 +608,9 @@ def main():
         return
     if args.workload == "dfa_mask":
         bench_dfa_mask(args, torch)
+        return
+    if args.workload == "lm_head":
+        bench_lm_head(args, torch)
         return
     if args.calibrate_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device=d)  # 256 MiB

@@ -10,15 +10,16 @@
 //   tokens x one 32-wide k block, with the quants in the order the matrix
 //   cores read them (one 16-byte load per lane per block) and the 32 scales
 //   permuted to the rows each lane's accumulators hold;
-// - mmvq_q8_0_kernel: per wavefront 32 tokens x 64 batch columns. Each k block
-//   is two v_mfma_i32_32x32x32_i8, giving the exact integer dot of every
+// - mmvq_q8_0_kernel: per wavefront 32 tokens x 32 batch columns. Each k block
+//   is one v_mfma_i32_32x32x32_i8, giving the exact integer dot of every
 //   (token, column) pair; the float accumulation then follows the reference
 //   kernel exactly (four accumulators by b % 4, fmaf(d_w * d_x, dot, acc),
 //   then (A0 + A2) + (A1 + A3)), so y is the reference's to the last bit.
 //
 // Bound: HBM (34 bytes per 32 weights, read once; activations and y are small
-// beside them) and, at 64 columns, the VALU's three operations per
-// (token, column, block) that the reference's float order needs.
+// beside them) and, as the batch grows, the VALU's operations per
+// (token, column, block) that the reference's float order needs (convert the
+// integer dot, scale product, fused multiply-add).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -32,7 +33,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kQ81Bytes = 36;       // {f16 d, f16 sum, int8 qs[32]} (common_types.cuh:8-11)
 constexpr int kQ80Bytes = 34;       // {f16 d, int8 qs[32]} (common_types.cuh:13-16)
 constexpr int kPackedBlock = 1088;  // 32 tokens x one k block: 64 lanes x 16 quant bytes, then 32 f16 scales
-constexpr int kColsPerBlock = 64;   // batch columns per workgroup: two 32-column MFMA tiles
 constexpr int kGroupsPerBlock = 4;  // token groups (wavefronts) per workgroup
 constexpr int kThreads = 256;
 
@@ -99,61 +99,138 @@ __global__ __launch_bounds__(kThreads) void pack_q8_0_kernel(const uint8_t* __re
   }
 }
 
-// mmvq_q8_0_cuda_kernel (quant_gemv_standard.cu:425-513) for 64 columns x 128
-// tokens per workgroup; each wavefront owns one group of 32 tokens and both
-// column tiles. No block barriers: wavefronts past the last group return.
+// mmvq_q8_0_cuda_kernel (quant_gemv_standard.cu:425-513) for 32 columns x
+// 128 tokens per workgroup; each wavefront owns one group of 32 tokens. With
+// a batch above 32 columns, the workgroups of one token range sit 8 apart in
+// launch order: workgroups go round-robin over the 8 XCDs, so they run on
+// the same XCD at about the same time and the second reads the weights from
+// that XCD's L2 instead of HBM.
+// - The activations of a group of four k blocks are staged once per
+//   workgroup in LDS (double-buffered, one barrier per group): quants as
+//   [k block][half g][column][16 bytes], scales converted to float.
+// - Each wavefront loads the next group's weights (one 16-byte load per lane
+//   per block, plus 32 bytes of scales) while it computes the current one.
+// Wavefronts past the last token group skip the arithmetic and stores but
+// keep taking part in the staging and the barriers.
+constexpr int kGroupBlocks = 4;  // k blocks per pipeline step (one per accumulator)
+
 __global__ __launch_bounds__(kThreads) void mmvq_q8_0_kernel(float* __restrict__ y, const uint8_t* __restrict__ wp,
                                                              const uint8_t* __restrict__ x, uint32_t m, uint32_t nb,
-                                                             uint32_t batch) {
-  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const uint32_t tg = blockIdx.x * kGroupsPerBlock + wave;
-  if (tg >= (m + 31u) / 32u) return;
+                                                             uint32_t batch, uint32_t ncb) {
+  constexpr int TILES = 1;
+  constexpr int COLS = 32 * TILES;
+  __shared__ __align__(16) uint4 s_xq[2][kGroupBlocks][2][COLS];  // quant halves
+  __shared__ float s_xd[2][kGroupBlocks][COLS];                   // scales as float
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  // token block tb and column block cb: in each run of 8 * ncb workgroups,
+  // workgroup 8 c + i holds token block i of the run and column block c
+  uint32_t tb, cb;
+  {
+    const uint32_t per = 8u * ncb, full = (gridDim.x / per) * per;
+    if (blockIdx.x < full) {
+      const uint32_t run = blockIdx.x / per, r = blockIdx.x - run * per;
+      tb = run * 8u + (r & 7u);
+      cb = r >> 3;
+    } else {
+      const uint32_t r = blockIdx.x - full;
+      tb = (full / per) * 8u + r / ncb;
+      cb = r - (r / ncb) * ncb;
+    }
+  }
+  const uint32_t tg = tb * kGroupsPerBlock + wave;
+  const bool live = tg < (m + 31u) / 32u;
   const uint32_t g = lane >> 5, j = lane & 31u;
-  const uint32_t c0 = blockIdx.y * kColsPerBlock;
-  // this lane's B-operand columns, clamped into the batch (their results are not stored)
-  const uint32_t colA = min(c0 + j, batch - 1u), colB = min(c0 + 32u + j, batch - 1u);
-  const uint8_t* xa = x + (size_t)colA * nb * kQ81Bytes;
-  const uint8_t* xb = x + (size_t)colB * nb * kQ81Bytes;
-  const uint8_t* wg = wp + (size_t)tg * nb * kPackedBlock;
+  const uint32_t c0 = cb * COLS;
+  const uint32_t ngroups = nb / kGroupBlocks;
 
-  float acc[2][4][16];
+  // staging: thread t < COLS * 4 copies the q8_1 block (column t / 4, block t % 4) of each group
+  const bool stager = tid < (uint32_t)(COLS * kGroupBlocks);
+  const uint32_t st_col = tid / kGroupBlocks, st_kb = tid % kGroupBlocks;
+  const uint8_t* st_src = x + (size_t)min(c0 + st_col, batch - 1u) * nb * kQ81Bytes + (size_t)st_kb * kQ81Bytes;
+  uint32_t xr[9];
+  auto stage_load = [&](uint32_t grp) {
+    if (stager) {
+      const uint32_t* p = (const uint32_t*)(st_src + (size_t)grp * kGroupBlocks * kQ81Bytes);  // 4-byte aligned
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+      for (int i = 0; i < 9; ++i) xr[i] = p[i];
+    }
+  };
+  auto stage_store = [&](int buf) {
+    if (stager) {
+      s_xd[buf][st_kb][st_col] = half_to_float((uint16_t)(xr[0] & 0xffffu));
+      s_xq[buf][st_kb][0][st_col] = make_uint4(xr[1], xr[2], xr[3], xr[4]);
+      s_xq[buf][st_kb][1][st_col] = make_uint4(xr[5], xr[6], xr[7], xr[8]);
+    }
+  };
+
+  const uint8_t* wg = wp + (size_t)(live ? tg : 0u) * nb * kPackedBlock;
+  v4i wa[kGroupBlocks];
+  uint4 ws0[kGroupBlocks], ws1[kGroupBlocks];
+  auto weight_load = [&](uint32_t grp) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < kGroupBlocks; ++q) {
+      const uint8_t* blk = wg + (size_t)(grp * kGroupBlocks + q) * kPackedBlock;
+      wa[q] = *(const v4i*)(blk + 16 * lane);
+      ws0[q] = *(const uint4*)(blk + 1024 + 32 * g);
+      ws1[q] = *(const uint4*)(blk + 1024 + 32 * g + 16);
+    }
+  };
+
+  float acc[TILES][kGroupBlocks][16];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int q = 0; q < kGroupBlocks; ++q)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[t][q][r] = 0.0f;
   const v16i zero = {};
 
-  for (uint32_t b0 = 0; b0 < nb; b0 += 4) {  // nb is a multiple of 4
+  stage_load(0);
+  stage_store(0);
+  if (live) weight_load(0);
+  __syncthreads();
+  for (uint32_t grp = 0; grp < ngroups; ++grp) {
+    const int buf = grp & 1;
+    v4i ca[kGroupBlocks];
+    uint4 cs0[kGroupBlocks], cs1[kGroupBlocks];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {  // block b0 + q goes to accumulator q = b % 4
-      const uint8_t* blk = wg + (size_t)(b0 + q) * kPackedBlock;
-      const v4i a = *(const v4i*)(blk + 16 * lane);
-      const uint4 s0 = *(const uint4*)(blk + 1024 + 32 * g);
-      const uint4 s1 = *(const uint4*)(blk + 1024 + 32 * g + 16);
-      const uint32_t* pa = (const uint32_t*)(xa + (size_t)(b0 + q) * kQ81Bytes);  // 4-byte aligned
-      const uint32_t* pb = (const uint32_t*)(xb + (size_t)(b0 + q) * kQ81Bytes);
-      const v4i ba = {(int)pa[1 + 4 * g], (int)pa[2 + 4 * g], (int)pa[3 + 4 * g], (int)pa[4 + 4 * g]};
-      const v4i bb = {(int)pb[1 + 4 * g], (int)pb[2 + 4 * g], (int)pb[3 + 4 * g], (int)pb[4 + 4 * g]};
-      const float dxa = half_to_float((uint16_t)(pa[0] & 0xffffu));
-      const float dxb = half_to_float((uint16_t)(pb[0] & 0xffffu));
-      const v16i da = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, ba, zero, 0, 0, 0);
-      const v16i db = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bb, zero, 0, 0, 0);
-      const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    for (int q = 0; q < kGroupBlocks; ++q) {
+      ca[q] = wa[q];
+      cs0[q] = ws0[q];
+      cs1[q] = ws1[q];
+    }
+    const bool more = grp + 1 < ngroups;
+    if (more) {
+      stage_load(grp + 1);
+      if (live) weight_load(grp + 1);
+    }
+    if (live) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float dw = half_to_float((uint16_t)(sw[r / 2] >> (16 * (r % 2))));
-        acc[0][q][r] = __builtin_fmaf(dw * dxa, (float)da[r], acc[0][q][r]);
-        acc[1][q][r] = __builtin_fmaf(dw * dxb, (float)db[r], acc[1][q][r]);
+      for (int q = 0; q < kGroupBlocks; ++q) {
+        const uint32_t sw[8] = {cs0[q].x, cs0[q].y, cs0[q].z, cs0[q].w, cs1[q].x, cs1[q].y, cs1[q].z, cs1[q].w};
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) {
+          const uint4 bq = s_xq[buf][q][g][32 * t + j];
+          const float dx = s_xd[buf][q][32 * t + j];
+          const v4i bv = {(int)bq.x, (int)bq.y, (int)bq.z, (int)bq.w};
+          const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca[q], bv, zero, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float dw = half_to_float((uint16_t)(sw[r / 2] >> (16 * (r % 2))));
+            acc[t][q][r] = __builtin_fmaf(dw * dx, (float)d[r], acc[t][q][r]);
+          }
+        }
       }
     }
+    if (more) stage_store(buf ^ 1);
+    __syncthreads();
   }
+  if (!live) return;
 
   // (A0 + A2) + (A1 + A3); registers 4 q' .. 4 q' + 3 hold four consecutive tokens
   const bool vec = (m & 3u) == 0u;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < TILES; ++t) {
     const uint32_t col = c0 + 32u * t + j;
     if (col >= batch) continue;
     float* yrow = y + (size_t)col * m;
@@ -216,10 +293,11 @@ extern "C" int oxs_mmvq_q8_0(float* y, const void* w_packed, const void* x_q8_1,
   if (k % 128u != 0) return OXS_ERR_UNSUPPORTED;
   if (!y || !w_packed || !x_q8_1) return OXS_ERR_INVALID_ARGUMENT;
   const uint32_t groups = (m + 31u) / 32u;
-  const dim3 grid((groups + oxs_lm::kGroupsPerBlock - 1) / oxs_lm::kGroupsPerBlock,
-                  (batch + oxs_lm::kColsPerBlock - 1) / oxs_lm::kColsPerBlock);
-  if (grid.y > 65535u) return OXS_ERR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL(oxs_lm::mmvq_q8_0_kernel, grid, dim3(oxs_lm::kThreads), 0, (hipStream_t)stream, y,
-                     (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, k / 32u, batch);
+  const uint32_t gx = (groups + oxs_lm::kGroupsPerBlock - 1) / oxs_lm::kGroupsPerBlock;
+  const uint32_t ncb = (batch + 31u) / 32u;  // 32-column blocks
+  const uint64_t grid = (uint64_t)gx * ncb;
+  if (grid > 0x7fffffffull) return OXS_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(oxs_lm::mmvq_q8_0_kernel, dim3((uint32_t)grid), dim3(oxs_lm::kThreads), 0, (hipStream_t)stream,
+                     y, (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, k / 32u, batch, ncb);
   return launch_status();
 }
