@@ -398,7 +398,7 @@ size_t oxs_q8_0_packed_bytes(uint32_t m, uint32_t k);
 /* Repacks GGUF Q8_0 rows (w, [m][k / 32] 34-byte blocks) into the packed
  * layout, once at model load. k must be a multiple of 128
  * (OXS_ERR_UNSUPPORTED otherwise). No counterpart in the reference, whose
- * kernel reads the GGUF blocks directly. */
+ * kernel reads the GGUF blocks directly. w_packed must be 16-byte aligned. */
 int oxs_pack_q8_0(const void* w, uint32_t m, uint32_t k, void* w_packed, void* stream);
 
 /* launch_cuda_mmvq_q8_0 (kernels/launch_wrappers.cu:156-200,
@@ -408,7 +408,8 @@ int oxs_pack_q8_0(const void* w, uint32_t m, uint32_t k, void* w_packed, void* s
  * for bit: per block b the exact integer dot of the 32 quants, accumulated as
  * A[b % 4] = fmaf(d_w * d_x, (float)dot, A[b % 4]) in increasing b, then
  * (A0 + A2) + (A1 + A3). m == 0 or batch == 0 does nothing; k must be a
- * multiple of 128. */
+ * multiple of 128. w_packed must be 16-byte aligned, x_q8_1 and y 4-byte
+ * aligned (OXS_ERR_INVALID_ARGUMENT otherwise). */
 int oxs_mmvq_q8_0(float* y, const void* w_packed, const void* x_q8_1, uint32_t m, uint32_t k, uint32_t batch,
                   void* stream);
 

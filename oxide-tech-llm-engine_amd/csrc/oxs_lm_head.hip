@@ -116,7 +116,7 @@ constexpr int kGroupBlocks = 4;  // k blocks per pipeline step (one per accumula
 
 __global__ __launch_bounds__(kThreads) void mmvq_q8_0_kernel(float* __restrict__ y, const uint8_t* __restrict__ wp,
                                                              const uint8_t* __restrict__ x, uint32_t m, uint32_t nb,
-                                                             uint32_t batch, uint32_t ncb) {
+                                                             uint32_t batch, uint32_t ncb, uint32_t vec_out) {
   constexpr int TILES = 1;
   constexpr int COLS = 32 * TILES;
   __shared__ __align__(16) uint4 s_xq[2][kGroupBlocks][2][COLS];  // quant halves
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void mmvq_q8_0_kernel(float* __restrict__
   if (!live) return;
 
   // (A0 + A2) + (A1 + A3); registers 4 q' .. 4 q' + 3 hold four consecutive tokens
-  const bool vec = (m & 3u) == 0u;
+  const bool vec = vec_out != 0u;  // m % 4 == 0 and y 16-byte aligned: float4 stores
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
     const uint32_t col = c0 + 32u * t + j;
@@ -254,6 +254,70 @@ __global__ __launch_bounds__(kThreads) void mmvq_q8_0_kernel(float* __restrict__
   }
 }
 
+// The same product for batches of at most four columns, where a 32-column
+// MFMA tile would be mostly idle (eight columns was measured slower than the
+// MFMA kernel). Each workgroup first stages the whole of x
+// (NC columns x every k block) in LDS, then each wavefront walks its 32
+// tokens with no further barrier: lane (j, g) takes 16 quant bytes of token j
+// per block (the packed layout's MFMA order), four dot4 products per column,
+// and the lane pair (j, j + 32) adds its halves into the block's exact
+// integer dot. The float accumulation is the reference's, as above. Bound:
+// HBM.
+template <int NC>
+__global__ __launch_bounds__(kThreads) void mmvq_q8_0_small_kernel(float* __restrict__ y,
+                                                                   const uint8_t* __restrict__ wp,
+                                                                   const uint8_t* __restrict__ x, uint32_t m,
+                                                                   uint32_t nb, uint32_t batch) {
+  extern __shared__ __align__(16) uint8_t s_small[];
+  uint4* s_q = (uint4*)s_small;                              // [NC][nb][2] quant halves
+  float* s_d = (float*)(s_small + (size_t)NC * nb * 32);     // [NC][nb] scales
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  for (uint32_t i = tid; i < NC * nb; i += kThreads) {
+    const uint32_t c = i / nb, b = i - c * nb;
+    const uint32_t* p = (const uint32_t*)(x + ((size_t)min(c, batch - 1u) * nb + b) * kQ81Bytes);
+    s_d[i] = half_to_float((uint16_t)(p[0] & 0xffffu));
+    s_q[2 * i] = make_uint4(p[1], p[2], p[3], p[4]);
+    s_q[2 * i + 1] = make_uint4(p[5], p[6], p[7], p[8]);
+  }
+  __syncthreads();
+  const uint32_t tg = blockIdx.x * kGroupsPerBlock + wave;
+  if (tg >= (m + 31u) / 32u) return;
+  const uint32_t g = lane >> 5, j = lane & 31u;
+  // this token's scale: position 16 ((j / 4) % 2) + 4 (j / 8) + j % 4 of the permuted scales
+  const uint32_t sp = 16u * ((j >> 2) & 1u) + 4u * (j >> 3) + (j & 3u);
+  const uint8_t* wg = wp + (size_t)tg * nb * kPackedBlock;
+  float acc[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[c][q] = 0.0f;
+  for (uint32_t b0 = 0; b0 < nb; b0 += 4) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t b = b0 + q;
+      const uint8_t* blk = wg + (size_t)b * kPackedBlock;
+      const uint4 wq = *(const uint4*)(blk + 16 * lane);
+      const float dw = half_to_float(*(const uint16_t*)(blk + 1024 + 2 * sp));
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 xq = s_q[2 * (c * nb + b) + g];
+        int dot = __builtin_amdgcn_sdot4((int)wq.x, (int)xq.x, 0, false);
+        dot = __builtin_amdgcn_sdot4((int)wq.y, (int)xq.y, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)wq.z, (int)xq.z, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)wq.w, (int)xq.w, dot, false);
+        dot += __shfl_xor(dot, 32);
+        acc[c][q] = __builtin_fmaf(dw * s_d[c * nb + b], (float)dot, acc[c][q]);
+      }
+    }
+  }
+  const uint32_t tok = tg * 32u + j;
+  if (g == 0 && tok < m) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if ((uint32_t)c < batch) y[(size_t)c * m + tok] = (acc[c][0] + acc[c][2]) + (acc[c][1] + acc[c][3]);
+  }
+}
+
 }  // namespace oxs_lm
 
 static int launch_status() { return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP; }
@@ -262,6 +326,7 @@ extern "C" int oxs_quantize_q8_1(const float* x, uint32_t n, void* y_q8_1, void*
   const uint32_t nblocks = n / 32u;
   if (nblocks == 0) return OXS_OK;
   if (!x || !y_q8_1) return OXS_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)x & 3u) || ((uintptr_t)y_q8_1 & 1u)) return OXS_ERR_INVALID_ARGUMENT;  // float loads, half stores
   const uint32_t per = oxs_lm::kThreads / 32;
   hipLaunchKernelGGL(oxs_lm::quantize_q8_1_kernel, dim3((nblocks + per - 1) / per), dim3(oxs_lm::kThreads), 0,
                      (hipStream_t)stream, x, nblocks, (uint8_t*)y_q8_1);
@@ -277,6 +342,7 @@ extern "C" int oxs_pack_q8_0(const void* w, uint32_t m, uint32_t k, void* w_pack
   if (k == 0 || k % 128u != 0) return OXS_ERR_UNSUPPORTED;
   if (m == 0) return OXS_OK;
   if (!w || !w_packed) return OXS_ERR_INVALID_ARGUMENT;
+  if ((uintptr_t)w_packed & 15u) return OXS_ERR_INVALID_ARGUMENT;  // 16-byte stores
   const uint32_t nb = k / 32u;
   const uint64_t pieces = (uint64_t)((m + 31u) / 32u) * nb;
   const uint64_t per = oxs_lm::kThreads / 64;
@@ -292,12 +358,33 @@ extern "C" int oxs_mmvq_q8_0(float* y, const void* w_packed, const void* x_q8_1,
   if (m == 0 || k == 0 || batch == 0) return OXS_OK;  // as launch_cuda_mmvq_q8_0's early return
   if (k % 128u != 0) return OXS_ERR_UNSUPPORTED;
   if (!y || !w_packed || !x_q8_1) return OXS_ERR_INVALID_ARGUMENT;
+  // 16-byte weight loads, 4-byte activation loads, 4-byte stores
+  if (((uintptr_t)w_packed & 15u) || ((uintptr_t)x_q8_1 & 3u) || ((uintptr_t)y & 3u)) return OXS_ERR_INVALID_ARGUMENT;
+  const uint32_t vec_out = (m % 4u == 0u && ((uintptr_t)y & 15u) == 0u) ? 1u : 0u;
   const uint32_t groups = (m + 31u) / 32u;
   const uint32_t gx = (groups + oxs_lm::kGroupsPerBlock - 1) / oxs_lm::kGroupsPerBlock;
+  const uint32_t nc_small = batch <= 1u ? 1u : batch <= 2u ? 2u : 4u;  // columns the small kernel stages
+  if (batch <= 4u && (size_t)nc_small * (k / 32u) * 36u <= 65536u) {    // the whole of x fits in LDS
+    const uint32_t nb = k / 32u;
+    const size_t lds = (size_t)nc_small * nb * 36u;
+    const dim3 g1(gx);
+    switch (batch) {
+      case 1: hipLaunchKernelGGL(oxs_lm::mmvq_q8_0_small_kernel<1>, g1, dim3(oxs_lm::kThreads), lds,
+                                 (hipStream_t)stream, y, (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, nb,
+                                 batch); break;
+      case 2: hipLaunchKernelGGL(oxs_lm::mmvq_q8_0_small_kernel<2>, g1, dim3(oxs_lm::kThreads), lds,
+                                 (hipStream_t)stream, y, (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, nb,
+                                 batch); break;
+      default: hipLaunchKernelGGL(oxs_lm::mmvq_q8_0_small_kernel<4>, g1, dim3(oxs_lm::kThreads), lds,
+                                  (hipStream_t)stream, y, (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, nb,
+                                  batch); break;
+    }
+    return launch_status();
+  }
   const uint32_t ncb = (batch + 31u) / 32u;  // 32-column blocks
   const uint64_t grid = (uint64_t)gx * ncb;
   if (grid > 0x7fffffffull) return OXS_ERR_INVALID_ARGUMENT;
   hipLaunchKernelGGL(oxs_lm::mmvq_q8_0_kernel, dim3((uint32_t)grid), dim3(oxs_lm::kThreads), 0, (hipStream_t)stream,
-                     y, (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, k / 32u, batch, ncb);
+                     y, (const uint8_t*)w_packed, (const uint8_t*)x_q8_1, m, k / 32u, batch, ncb, vec_out);
   return launch_status();
 }

@@ -211,8 +211,12 @@ def test_gpu_quantize_matches_oracle(torch_gpu, batch, k):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m,k,batch", [(1, 128, 1), (33, 128, 3), (130, 256, 64), (1001, 896, 65),
-                                       (4099, 512, 130), (2050, 4096, 7)])
+                                       (4099, 512, 130), (2050, 4096, 7), (517, 4096, 1), (300, 1024, 2),
+                                       (129, 4096, 4), (70, 16384, 4), (64, 16384, 5), (257, 4096, 6), (96, 4096, 8),
+                                       (40, 8192, 8), (33, 128, 9)])
 def test_gpu_mmvq_matches_oracle(torch_gpu, m, k, batch):
+    # batch <= 4 with x (staged for 1, 2 or 4 columns) within 64 KB of LDS takes the
+    # small-batch kernel; (70, 16384, 4) and batch > 4 take the MFMA kernel
     from oxide_sampler import LmHeadQ8_0, quantize_q8_1
     rng = np.random.default_rng(m + 3 * k + 7 * batch)
     w, x = random_case(rng, m, k, batch)
@@ -272,4 +276,32 @@ def test_gpu_lm_head_errors(torch_gpu):
     assert lib.oxs_quantize_q8_1(None, 31, None, None) == 0  # fewer than 32 values: no block
     with pytest.raises(ValueError):
         LmHeadQ8_0(np.zeros(10 * 3 * 34, np.uint8), 10, 96)
-    del ctypes
+    # misaligned pointers are refused before any launch
+    buf = torch_gpu.zeros(4096, dtype=torch_gpu.uint8, device="cuda")
+    p = buf.data_ptr()
+    assert lib.oxs_mmvq_q8_0(ctypes.c_void_p(p), ctypes.c_void_p(p + 8), ctypes.c_void_p(p), 1, 128, 1, None) == -1
+    assert lib.oxs_mmvq_q8_0(ctypes.c_void_p(p), ctypes.c_void_p(p), ctypes.c_void_p(p + 2), 1, 128, 1, None) == -1
+    assert lib.oxs_pack_q8_0(ctypes.c_void_p(p), 1, 128, ctypes.c_void_p(p + 4), None) == -1
+    assert lib.oxs_quantize_q8_1(ctypes.c_void_p(p + 1), 32, ctypes.c_void_p(p), None) == -1
+
+
+@pytest.mark.gpu
+def test_gpu_mmvq_unaligned_output_rows(torch_gpu):
+    # y at an offset of one float (4-byte aligned only) and m % 4 == 0: the scalar store path
+    import ctypes
+    from oxide_sampler import LmHeadQ8_0, load_library, quantize_q8_1
+    m, k, batch = 96, 128, 3
+    rng = np.random.default_rng(5)
+    w, x = random_case(rng, m, k, batch)
+    print("\n[case] mmvq_q8_0 into y + 1 float", flush=True)
+    head = LmHeadQ8_0(w, m, k)
+    xq = quantize_q8_1(_to_dev(torch_gpu, x))
+    y = torch_gpu.full((batch * m + 4,), -7.0, dtype=torch_gpu.float32, device="cuda")
+    lib = load_library()
+    assert lib.oxs_mmvq_q8_0(ctypes.c_void_p(y.data_ptr() + 4), ctypes.c_void_p(head.packed.data_ptr()),
+                             ctypes.c_void_p(xq.data_ptr()), m, k, batch, None) == 0
+    torch_gpu.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = oracle.mmvq_q8_0_host(w, oracle.quantize_q8_1_host(x), m, k, batch).reshape(-1)
+    np.testing.assert_array_equal(got[1:1 + batch * m].view(np.uint32), want.view(np.uint32))
+    assert got[0] == -7.0 and (got[1 + batch * m:] == -7.0).all()
