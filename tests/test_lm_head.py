@@ -305,3 +305,27 @@ def test_gpu_mmvq_unaligned_output_rows(torch_gpu):
     want = oracle.mmvq_q8_0_host(w, oracle.quantize_q8_1_host(x), m, k, batch).reshape(-1)
     np.testing.assert_array_equal(got[1:1 + batch * m].view(np.uint32), want.view(np.uint32))
     assert got[0] == -7.0 and (got[1 + batch * m:] == -7.0).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,softcap", [(3, 0.0), (40, 0.0), (40, 30.0)])
+def test_gpu_decode_head_chain_matches_oracle(torch_gpu, batch, softcap):
+    # hidden states -> q8_1 -> LM head -> sampler (config 2's chain), every step on the
+    # device with no host copy between them, against the oracle's chain on the same inputs
+    from harness import compare, run_gpu, run_oracle
+    from oxide_sampler import LmHeadQ8_0, quantize_q8_1
+    from oxide_sampler import workloads as wl
+    m, k = 5003, 512
+    rng = np.random.default_rng(100 + batch)
+    w8, x = random_case(rng, m, k, batch)
+    print(f"\n[case] decode head chain batch={batch} softcap={softcap}", flush=True)
+    head = LmHeadQ8_0(w8, m, k)
+    logits_dev = head.project(quantize_q8_1(_to_dev(torch_gpu, x)))
+    w = wl.config2(batch=batch, vocab=m)
+    w.logits = oracle.mmvq_q8_0_host(w8, oracle.quantize_q8_1_host(x), m, k, batch)
+    if softcap:
+        w.extra["softcap"] = softcap
+    gpu = run_gpu(w, torch_gpu, logits_dev=logits_dev)
+    ref = run_oracle(w)
+    compare(gpu, ref, 1e-5, "decode head chain")
+    assert (gpu.status == 0).all()
