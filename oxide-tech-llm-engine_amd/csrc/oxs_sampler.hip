@@ -911,9 +911,11 @@ __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowX
       if (r.any_special) build_table(p, r, row, c0, c1, table);
       for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
         const float y = transformed_logit<DT>(p, r, row, i, c0, table);
-        // the stream kernel's write-back has no DRY: the DRY ids' values here
-        if (d == 0 && r.dry && p.logits_out && (table[i - c0] & kDryFlag))
-          p.logits_out[(size_t)row * p.logits_out_ld + i] = y;
+        // the row's whole write-back again: the stream kernel's has no DRY, and
+        // a chunk whose sparse-stage ids overflowed its LDS hash (a record
+        // marked bad, which is what sends the row here) wrote values without
+        // some of its penalties
+        if (d == 0 && p.logits_out) p.logits_out[(size_t)row * p.logits_out_ld + i] = y;
         const uint32_t k = cand_key(y);
         if (!k) continue;
         const uint64_t key = comp_key(k, i);

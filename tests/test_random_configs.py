@@ -1,0 +1,138 @@
+"""Randomised parity sweep: every SamplingConfig stage switched on at random, per row.
+
+Each case draws a batch shape, a logits dtype (f32 or bf16), a logit
+distribution (Gaussian, heavy spikes, long runs of equal values, -inf rows), a
+grammar mask (none, per row or shared), a softcap, histories of random
+length, and for every row a SamplingConfig whose fields are each enabled with
+probability 1/2 at random values (sampler.rs:16-73). The HIP path must match
+the oracle exactly: tokens, status, kept ids and probabilities, history, mu.
+Rows the device declines (top_k > 1024, DRY slices > 1024) report
+OXS_ROW_UNSUPPORTED in both.
+"""
+import numpy as np
+import pytest
+
+from harness import compare, run_gpu, run_oracle
+from oxide_sampler import MirostatMode
+from oxide_sampler import workloads as wl
+
+RTOL_F32 = 1e-5
+RTOL_BF16 = 1e-3
+
+
+def banner(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+def random_config(rng, V):
+    kw = {}
+    coin = lambda: rng.random() < 0.5  # noqa: E731
+    kw["temperature"] = float(rng.choice([0.0, 1e-7, 0.3, 0.7, 1.0, 1.6])) if coin() else 1.0
+    if coin():
+        kw["top_k"] = int(rng.choice([1, 2, 40, 50, 255, 256, 300, 1024]))
+    if coin():
+        kw["top_p"] = float(rng.choice([0.5, 0.9, 0.95, 0.999]))
+    if coin():
+        kw["min_p"] = float(rng.choice([0.01, 0.05, 0.2]))
+    if coin():
+        kw["tfs_z"] = float(rng.choice([0.5, 0.9, 0.99]))
+    if coin():
+        kw["typical_p"] = float(rng.choice([0.2, 0.8, 0.95]))
+    if coin():
+        kw["xtc_threshold"] = float(rng.choice([0.01, 0.1, 0.3]))
+        kw["xtc_probability"] = float(rng.choice([0.3, 1.0]))
+    if rng.random() < 0.2:
+        kw["mirostat_mode"] = MirostatMode.V1 if coin() else MirostatMode.V2
+        kw["mirostat_tau"] = float(rng.choice([2.0, 5.0]))
+        kw["mirostat_eta"] = float(rng.choice([0.1, 0.3]))
+    if rng.random() < 0.25:
+        kw["dry_multiplier"] = float(rng.choice([0.5, 1.5]))
+        kw["dry_base"] = float(rng.choice([1.1, 1.75]))
+        kw["dry_allowed_length"] = int(rng.choice([0, 2, 3]))
+        kw["dry_range"] = int(rng.choice([16, 128, 1024]))
+    if coin():
+        kw["repeat_penalty"] = float(rng.choice([0.9, 1.1, 1.3]))
+        kw["repeat_last_n"] = int(rng.choice([0, 8, 64, 512]))
+    if coin():
+        kw["frequency_penalty"] = float(rng.choice([-0.3, 0.2, 0.6]))
+    if coin():
+        kw["presence_penalty"] = float(rng.choice([-0.2, 0.3]))
+    if coin():
+        kw["penalize_nl"] = True
+        kw["newline_penalty"] = float(rng.choice([0.5, 2.0]))
+    if coin():
+        ids = rng.integers(0, V + 3, size=int(rng.integers(1, 6)))
+        kw["logit_biases"] = {int(i): float(rng.choice([-5.0, -0.5, 0.75, 4.0])) for i in ids}
+    if coin():
+        kw["banned_tokens"] = {int(i) for i in rng.integers(0, V + 3, size=int(rng.integers(1, 6)))}
+    return wl.disabled_config(**kw)
+
+
+def random_workload(seed):
+    rng = np.random.default_rng(seed)
+    B = int(rng.choice([1, 3, 8, 17, 33]))
+    V = int(rng.choice([5, 100, 1000, 4097, 20000, 65537]))
+    kind = rng.integers(0, 3)
+    x = rng.standard_normal((B, V)).astype(np.float32) * np.float32(rng.choice([0.5, 2.0, 4.0]))
+    if kind == 1:  # a heavy tail of spikes
+        x[rng.random((B, V)) < 0.01] += np.float32(8.0)
+    elif kind == 2 and V > 20:  # long runs of equal values: ties broken by the lower id
+        x[:, V // 4: V // 2] = np.float32(1.5)
+    if B > 2 and rng.random() < 0.5:
+        x[1, :] = -np.inf
+    bf16 = rng.random() < 0.3
+    logits = wl.f32_to_bf16_bits(x) if bf16 else x
+    cap = 1100
+    history = rng.integers(0, V, size=(B, cap), dtype=np.uint32)
+    history[:, ::9] = np.uint32(min(10, V - 1))
+    hlen = rng.integers(0, 1090, size=B).astype(np.uint32)
+    for b in range(B):
+        n = int(hlen[b])
+        if n >= 30 and rng.random() < 0.5:  # repeated motifs: DRY n-gram matches
+            history[b, n - 30:n] = np.tile(rng.integers(0, V, size=3, dtype=np.uint32), 10)
+    mask = None
+    mchoice = rng.integers(0, 3)
+    if mchoice:
+        words = (V + 31) // 32
+        bits = rng.random((1 if mchoice == 2 else B, words * 32)) < rng.choice([0.03, 0.5])
+        bits[:, int(rng.integers(0, V))] = True
+        mask = np.packbits(bits.astype(np.uint8), axis=1, bitorder="little").view(np.uint32)[:, :words].copy()
+    configs = [random_config(rng, V) for _ in range(B)]
+    w = wl.Workload(name=f"random seed={seed} B={B} V={V}", logits=logits, dtype="bf16" if bf16 else "f32",
+                    configs=configs, history=history, history_len=hlen, uniforms=wl.xorshift_uniforms(B, seed),
+                    mask=mask, mu=np.full(B, 10.0, np.float32))
+    if rng.random() < 0.3:
+        w.extra["softcap"] = float(rng.choice([5.0, 30.0]))
+    return w, mchoice == 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configs(torch_gpu, seed):
+    w, shared = random_workload(1000 + seed)
+    banner(f"{w.name} {w.dtype} mask={'shared' if shared else w.mask is not None} "
+           f"softcap={w.extra.get('softcap', 0)}")
+    g = run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=1024, shared_mask=shared)
+    r = run_oracle(w, kept_ld=1024, logits_out=True, shared_mask=shared)
+    compare(g, r, RTOL_BF16 if w.dtype == "bf16" else RTOL_F32, w.name)
+
+
+@pytest.mark.gpu
+def test_logits_out_when_penalty_ids_overflow_the_chunk_hash(torch_gpu):
+    # V = 1000 is one stream chunk; a whole-history window of 900 distinct ids overflows its
+    # 256-slot LDS hash, so the row goes to the exact path, which must write every id of
+    # logits_out with its penalties (sampler.rs:207-245)
+    rng = np.random.default_rng(77)
+    B, V = 4, 1000
+    logits = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    history = np.stack([rng.permutation(V)[:900].astype(np.uint32) for _ in range(B)])
+    configs = [wl.disabled_config(frequency_penalty=0.6, presence_penalty=0.2, repeat_last_n=0),
+               wl.disabled_config(repeat_penalty=1.3, repeat_last_n=0, temperature=0.7),
+               wl.disabled_config(presence_penalty=-0.2, top_k=40, top_p=0.9),
+               wl.disabled_config(frequency_penalty=0.3, repeat_penalty=1.1, repeat_last_n=900, min_p=0.05)]
+    w = wl.Workload(name="hash overflow", logits=logits, dtype="f32", configs=configs, history=history,
+                    history_len=np.full(B, 900, np.uint32), uniforms=wl.xorshift_uniforms(B, 77))
+    banner("logits_out with 900 distinct penalty ids in one chunk")
+    g = run_gpu(w, torch_gpu, logits_out=True, record=False)
+    r = run_oracle(w, logits_out=True, record=False)
+    compare(g, r, RTOL_F32, w.name)
