@@ -37,6 +37,20 @@ constexpr int kGroupsPerBlock = 4;  // token groups (wavefronts) per workgroup
 constexpr int kThreads = 256;
 
 __device__ __forceinline__ float half_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// (float)half(lo or hi 16 bits of w) * x, rounded once, in one v_fma_mix_f32
+// (S0 read as f16, S1 as f32, S2 = 0): the widening is exact, so this equals
+// the multiply after a conversion, except that a zero product is +0; the
+// accumulators start at +0 and a +0 or -0 product leaves them equal.
+template <int HI>
+__device__ __forceinline__ float half_times(uint32_t w, float x) {
+  float d;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(x));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(x));
+  return d;
+}
 __device__ __forceinline__ uint16_t float_to_half(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 // Row i of the 32 x 32 MFMA output held in register r of a lane in half g
@@ -216,8 +230,8 @@ __global__ __launch_bounds__(kThreads) void mmvq_q8_0_kernel(float* __restrict__
           const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca[q], bv, zero, 0, 0, 0);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float dw = half_to_float((uint16_t)(sw[r / 2] >> (16 * (r % 2))));
-            acc[t][q][r] = __builtin_fmaf(dw * dx, (float)d[r], acc[t][q][r]);
+            const float dd = (r % 2) ? half_times<1>(sw[r / 2], dx) : half_times<0>(sw[r / 2], dx);
+            acc[t][q][r] = __builtin_fmaf(dd, (float)d[r], acc[t][q][r]);
           }
         }
       }
