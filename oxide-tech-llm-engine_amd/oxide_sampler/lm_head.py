@@ -37,7 +37,8 @@ def quantize_q8_1(x, out=None, stream=None):
     t = _torch()
     if x.dtype != t.float32 or not x.is_cuda:
         raise TypeError("x must be a float32 device tensor")
-    x = x.contiguous()
+    if not x.is_contiguous():  # a copy here would run on the current stream, not on `stream`
+        raise ValueError("x must be contiguous")
     k = x.shape[-1]
     if k % 32:
         raise ValueError("the last dimension must be a multiple of 32")
@@ -87,7 +88,9 @@ class LmHeadQ8_0:
         row_bytes = self.k // 32 * Q8_1_BYTES
         if x_q8_1.dtype != t.uint8 or not x_q8_1.is_cuda or x_q8_1.dim() != 2 or x_q8_1.shape[1] != row_bytes:
             raise ValueError(f"x_q8_1 must be a uint8 device tensor [batch, {row_bytes}]")
-        x = x_q8_1.contiguous()
+        if not x_q8_1.is_contiguous():
+            raise ValueError("x_q8_1 must be contiguous")
+        x = x_q8_1
         batch = x.shape[0]
         if out is None:
             out = t.empty(batch, self.m, dtype=t.float32, device=x.device)
