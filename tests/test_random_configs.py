@@ -136,3 +136,76 @@ def test_logits_out_when_penalty_ids_overflow_the_chunk_hash(torch_gpu):
     g = run_gpu(w, torch_gpu, logits_out=True, record=False)
     r = run_oracle(w, logits_out=True, record=False)
     compare(g, r, RTOL_F32, w.name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(5000, 5008))
+def test_random_decode_steps(torch_gpu, seed):
+    # oxs_decode_step over three steps with random configs (raw-argmax rows included) and
+    # the device rng: tokens, kept sets, history, mu, rng state and the per-row advance
+    import ctypes
+    import test_decode_loop as td
+    from oxide_sampler import BatchSampler, _abi, configs_to_array
+    from oxide_sampler._abi import OxsDecodeIo
+    t = torch_gpu
+    rng = np.random.default_rng(seed)
+    B, V, cap = int(rng.choice([3, 17, 40])), int(rng.choice([1000, 50001])), 1200
+    cfgs = []
+    for _ in range(B):
+        c = random_config(rng, V)
+        c.logit_biases, c.banned_tokens = {}, set()  # the decode loop's configs carry no lists
+        if rng.random() < 0.25:
+            c.temperature = float(rng.choice([0.0, 1e-6, -1.0]))
+        cfgs.append(c)
+    cfg_bytes = configs_to_array(cfgs, 10)[0]
+    history = rng.integers(0, V, size=(B, cap), dtype=np.uint32)
+    hlen = rng.integers(0, 1100, size=B).astype(np.uint32)
+    mu = np.full(B, 10.0, np.float32)
+    rng_state = np.array([(0x853C49E6748FEA9B + 977 * b * seed) & (2**64 - 1) or 1 for b in range(B)], np.uint64)
+    dec = {"current_token": rng.integers(0, V, size=B).astype(np.uint32),
+           "current_position": rng.integers(0, 5000, size=B).astype(np.int32),
+           "generated_count": rng.integers(0, 50, size=B).astype(np.uint32)}
+    d_cfg = td._to_dev(t, cfg_bytes)
+    d_hist, d_hlen, d_mu, d_rng = (td._to_dev(t, a) for a in (history, hlen, mu, rng_state))
+    d_dec = {k: td._to_dev(t, v) for k, v in dec.items()}
+    lib = _abi.load_library()
+    host = ctypes.c_void_p()
+    _abi.check(lib.oxs_host_alloc(8 * B, ctypes.byref(host)), "oxs_host_alloc")
+    s = BatchSampler(B, V, 1024)
+    try:
+        io = OxsDecodeIo(d_dec["current_token"].data_ptr(), d_dec["current_position"].data_ptr(),
+                         d_dec["generated_count"].data_ptr(), host.value)
+        out = {"tokens": t.zeros(B, dtype=t.int32, device="cuda"), "status": t.zeros(B, dtype=t.int32, device="cuda"),
+               "kept_count": t.zeros(B, dtype=t.int32, device="cuda"),
+               "kept_ids": t.zeros(B, 256, dtype=t.int32, device="cuda"),
+               "kept_probs": t.zeros(B, 256, dtype=t.float32, device="cuda")}
+        sent = int(np.uint32(td.SENT).view(np.int32))
+        for step in range(3):
+            banner(f"random decode seed={seed} B={B} V={V} step {step}")
+            x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+            x[rng.random((B, V)) < 0.003] += np.float32(6.0)
+            for k in ("kept_count", "kept_ids"):
+                out[k].fill_(sent)
+            out["kept_probs"].view(t.int32).fill_(sent)
+            s.sample(td._to_dev(t, x), d_cfg, history=d_hist, history_len=d_hlen, history_cap=cap, record=True,
+                     rng_state=d_rng, mirostat_mu=d_mu, kept_ld=256, decode=io, out=out)
+            t.cuda.synchronize()
+            ref = td.oracle_decode(cfg_bytes, x, history, hlen, mu, rng_state, dec, cap)
+            np.testing.assert_array_equal(td._u32(out["tokens"]), ref["tokens"])
+            np.testing.assert_array_equal(out["status"].cpu().numpy(), ref["status"])
+            np.testing.assert_array_equal(td._u32(out["kept_count"]), ref["kept_count"])
+            kid, kpr = td._u32(out["kept_ids"]), out["kept_probs"].cpu().numpy().view(np.uint32)
+            for b in range(B):
+                n = 256 if ref["kept_count"][b] == td.SENT else min(int(ref["kept_count"][b]), 256)
+                np.testing.assert_array_equal(kid[b, :n], ref["kept_ids"][b, :n])
+                np.testing.assert_array_equal(kpr[b, :n], ref["kept_probs"][b, :n].view(np.uint32))
+            np.testing.assert_array_equal(td._u32(d_hlen), hlen)
+            np.testing.assert_array_equal(td._u32(d_hist), history)
+            np.testing.assert_array_equal(d_mu.cpu().numpy().view(np.uint32), mu.view(np.uint32))
+            np.testing.assert_array_equal(d_rng.cpu().numpy().view(np.uint64), rng_state)
+            for k in dec:
+                np.testing.assert_array_equal(d_dec[k].cpu().numpy().view(dec[k].dtype), dec[k])
+    finally:
+        t.cuda.synchronize()
+        s.close()
+        lib.oxs_host_free(host)
