@@ -1920,7 +1920,11 @@ static uint32_t floor_pow2(uint32_t x) {
 }
 
 // Chunking: the largest per-block tile count that still gives >= 1024 blocks
-// (several per CU on 256 CUs), within kMaxChunk and kMaxChunks.
+// (several per CU on 256 CUs), within kMaxChunk and kMaxChunks, but no
+// smaller chunks than needed to keep a row at 64 wavefront records: past
+// that, each wavefront's share of the 2048-key union drops to 16 keys or
+// fewer and its threshold to the 8th lane maximum, and most rows of a small
+// batch would fail the top-M proof and take the exact re-scan.
 static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
   const uint32_t epl = dtype == OXS_DTYPE_F32 ? 4 : 8;
   const uint32_t tile = kThreads * epl;
@@ -1936,6 +1940,7 @@ static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
       if (slots == forced) best = slots;
       continue;
     }
+    if (best >= 0 && S * (uint32_t)kWavesPerBlock > 64u) break;
     best = slots;  // smaller slots keep overwriting while the grid stays small
     if ((uint64_t)B * S >= 1024) break;
   }
