@@ -42,6 +42,7 @@ namespace oxs {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / 64;
 constexpr int kUnionMax = 2048;   // candidate key slots per row
+constexpr int kUnionBig = 4096;   // ... for rows of more than 64 wavefront records (V > 16 chunks)
 constexpr int kTailArea = 4096;   // 64-bit words of tail LDS shared by the scatter, sort, exact-path table and chain scratch
 constexpr int kMaxM = 1024;       // largest max(top_k, 256) run on the device
 constexpr int kMaxChunk = 8192;   // logits per stream block
@@ -1466,7 +1467,7 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
 
 // ---------------------------------------------------------------- top-M selection
 
-constexpr int kPer = kUnionMax / kThreads;  // candidate key slots per tail thread
+constexpr int kPer = kUnionMax / kThreads;  // candidate key slots per tail thread (kUnionBig: twice as many)
 constexpr uint32_t kBigBucket = 64;         // largest bucket ranked by direct comparison
 static_assert(kBuckets == 4 * 64, "4 buckets per lane of a scanning wavefront");
 
@@ -1476,13 +1477,14 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t k, float vmax, float scal
 
 // Fallback selection: all kept register keys (bit q of vm) into tmp, a bitonic
 // sort, the first meff into out. Returns the number of kept keys.
-__device__ uint32_t sort_select(const uint64_t (&lk)[kPer], uint32_t vm, uint32_t M, uint64_t* tmp,
+template <int PER>
+__device__ uint32_t sort_select(const uint64_t (&lk)[PER], uint32_t vm, uint32_t M, uint64_t* tmp,
                                 uint64_t* out, TailShared& ts) {
   const uint32_t cnt = (uint32_t)__popc(vm);
   uint32_t n;
   uint32_t pos = block_excl_scan(cnt, &n, ts.scan_scratch);
 #pragma unroll
-  for (int q = 0; q < kPer; ++q)
+  for (int q = 0; q < PER; ++q)
     if ((vm >> q) & 1u) tmp[pos++] = lk[q];
   __syncthreads();
   const uint32_t meff = min(M, n);
@@ -1604,7 +1606,7 @@ __device__ void keys_to_chain(const uint64_t* keys, uint32_t n, uint32_t* ids, f
   __syncthreads();
 }
 
-template <int DT>
+template <int DT, int PER>
 // Leading arguments: what the first loads need, preloaded into SGPRs as in
 // stream_kernel.
 __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restrict__ wave_theta,
@@ -1613,7 +1615,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
                                                         const uint64_t* __restrict__ libm, uint32_t S, uint32_t cap_w,
                                                         uint32_t cap_shift, uint32_t rpx, uint32_t B, const Params p) {
   __shared__ __align__(16) uint64_t s_keys[kTailArea];  // bucket scatter / sort / exact-path table / chain scratch
-  static_assert(kTailArea >= kUnionMax && kTailArea * 2 >= kMaxChunk, "tail LDS area");
+  static_assert(kTailArea >= PER * kThreads && kTailArea * 2 >= kMaxChunk, "tail LDS area");
   __shared__ __align__(16) uint64_t s_top[kMaxM];       // sorted top-M keys (sort and exact paths)
   __shared__ __align__(16) uint32_t s_ids[kChainLd];
   __shared__ __align__(16) float s_pr[kChainLd];
@@ -1643,12 +1645,12 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
     const uint32_t w = lane + 64u * q;
     wr[q] = wave_theta[(size_t)row * W + (w < W ? w : W - 1u)];
   }
-  uint64_t lk[kPer];
-  uint32_t lc[kPer / 2];
+  uint64_t lk[PER];
+  uint32_t lc[PER / 2];
   const ulonglong2* lrow = (const ulonglong2*)(lists + (size_t)row * span);
   const uint32_t* wcrow = wave_count + (size_t)row * W;
 #pragma unroll
-  for (int q = 0; q < kPer / 2; ++q) {  // unconditional loads (clamped index): no branches between them
+  for (int q = 0; q < PER / 2; ++q) {  // unconditional loads (clamped index): no branches between them
     const uint32_t pair = tid + q * kThreads;
     const uint32_t at = 2u * pair < span ? pair : 0u;
     const ulonglong2 k2 = lrow[at];
@@ -1700,7 +1702,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   uint32_t valid = 0;
   uint64_t kmn = ~0ull;
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) {
+  for (int q = 0; q < PER; ++q) {
     const uint32_t slot = 2u * (tid + (q / 2) * kThreads) + (q & 1);
     const uint64_t k = lk[q];
     if (slot < span && (slot & (cap_w - 1u)) < lc[q / 2] && k != 0ull) {
@@ -1731,9 +1733,9 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   // 3. kept keys: at or above every wavefront threshold (when every
   // wavefront kept all, every valid key)
   uint32_t vm = 0;
-  const uint64_t (&yk)[kPer] = lk;
+  const uint64_t (&yk)[PER] = lk;
 #pragma unroll
-  for (int q = 0; q < kPer; ++q)
+  for (int q = 0; q < PER; ++q)
     if (((valid >> q) & 1u) && lk[q] >= theta_max) vm |= 1u << q;
 
   // 4. N >= M kept keys contain the row's top M. Keys are bucketed linearly
@@ -1750,7 +1752,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
                       scale <= __FLT_MAX__ && vmax <= __FLT_MAX__ && vmin >= -__FLT_MAX__;
   uint32_t meff = 0;
   int path = exact ? 2 : 1;  // 0 buckets, 1 sort, 2 exact re-scan
-  uint32_t bs[kPer];
+  uint32_t bs[PER];
   uint32_t* s_bstart = s_bstart_all[wave];
   uint32_t last = 0;
   if (linear) {
@@ -1758,7 +1760,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
     // slot issues its atomic (unkept ones add 0 to this lane's dummy counter)
     // so that the atomics go out back to back.
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
+    for (int q = 0; q < PER; ++q) {
       const bool on = (vm >> q) & 1u;
       const uint32_t b = on ? bucket_of(yk[q], vmax, scale) : (uint32_t)kBuckets + lane;
       bs[q] = b | (atomicAdd(&s_bcount[b], on ? 1u : 0u) << 16);  // bucket | slot inside the bucket
@@ -1792,11 +1794,11 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
       return;
     }
     const uint32_t span_k = s_bstart[last] + s_bcount[last];  // keys in buckets 0 .. last
-    uint32_t start[kPer];
+    uint32_t start[PER];
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) start[q] = s_bstart[min(bs[q] & 0xffffu, (uint32_t)kBuckets - 1)];
+    for (int q = 0; q < PER; ++q) start[q] = s_bstart[min(bs[q] & 0xffffu, (uint32_t)kBuckets - 1)];
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
+    for (int q = 0; q < PER; ++q) {
       if (((vm >> q) & 1u) && (bs[q] & 0xffffu) <= last) s_keys[start[q] + (bs[q] >> 16)] = yk[q];
     }
     __syncthreads();
@@ -1929,17 +1931,11 @@ static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
   const uint32_t epl = dtype == OXS_DTYPE_F32 ? 4 : 8;
   const uint32_t tile = kThreads * epl;
   int best = -1;
-  const char* env = getenv("OXS_SLOTS");
-  const int forced = env ? atoi(env) : 0;
   for (int slots = 8; slots >= 1; slots >>= 1) {
     const uint32_t ch = slots * tile;
     if (ch > (uint32_t)kMaxChunk) continue;
     const uint32_t S = (V + ch - 1) / ch;
     if (S > (uint32_t)kMaxChunks) continue;
-    if (forced) {
-      if (slots == forced) best = slots;
-      continue;
-    }
     if (best >= 0 && S * (uint32_t)kWavesPerBlock > 64u) break;
     best = slots;  // smaller slots keep overwriting while the grid stays small
     if ((uint64_t)B * S >= 1024) break;
@@ -1949,7 +1945,7 @@ static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
   g->CH = best * tile;
   g->S = (V + g->CH - 1) / g->CH;
   const uint32_t W = g->S * kWavesPerBlock;
-  g->cap_w = floor_pow2(min(32u, (uint32_t)kUnionMax / W));
+  g->cap_w = floor_pow2(min(32u, (uint32_t)(W > 64u ? kUnionBig : kUnionMax) / W));
   const uint32_t cw = (3u * 256u + W - 1) / W + 6u;
   g->c_w = max(1u, min(g->cap_w / 2, cw));
   return true;
@@ -1987,9 +1983,15 @@ static hipError_t launch_all(int slots, bool vec, bool mask, const Params& p, ui
   if (vec) e = mask ? launch_slots<SK, true, true>(slots, p, grid_a, st) : launch_slots<SK, true, false>(slots, p, grid_a, st);
   else e = mask ? launch_slots<SK, false, true>(slots, p, grid_a, st) : launch_slots<SK, false, false>(slots, p, grid_a, st);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((tail_kernel<KIND>), dim3(grid_b), dim3(kThreads), 0, st, (const uint64_t*)p.wave_theta,
-                     (const uint64_t*)p.lists, (const uint32_t*)p.wave_count, p.libm, p.S, p.cap_w, p.cap_shift, p.rpx,
-                     p.B, p);
+  // the row's candidate union: 2048 keys, or 4096 past 64 wavefront records
+  if ((uint64_t)p.S * kWavesPerBlock * p.cap_w > (uint64_t)kUnionMax)
+    hipLaunchKernelGGL((tail_kernel<KIND, kUnionBig / kThreads>), dim3(grid_b), dim3(kThreads), 0, st,
+                       (const uint64_t*)p.wave_theta, (const uint64_t*)p.lists, (const uint32_t*)p.wave_count, p.libm,
+                       p.S, p.cap_w, p.cap_shift, p.rpx, p.B, p);
+  else
+    hipLaunchKernelGGL((tail_kernel<KIND, kPer>), dim3(grid_b), dim3(kThreads), 0, st, (const uint64_t*)p.wave_theta,
+                       (const uint64_t*)p.lists, (const uint32_t*)p.wave_count, p.libm, p.S, p.cap_w, p.cap_shift,
+                       p.rpx, p.B, p);
   return hipGetLastError();
 }
 
@@ -2095,7 +2097,10 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
   s->limits.max_top_k = mtk;
   const size_t B = limits->max_batch;
   const size_t W = (size_t)oxs::kMaxChunks * oxs::kWavesPerBlock;
-  const size_t b_lists = B * oxs::kUnionMax * sizeof(uint64_t);
+  // rows over 16 chunks (more than 64 wavefront records) use the 4096-key union
+  const size_t b_lists =
+      B * (size_t)(limits->max_vocab > 16u * (uint32_t)oxs::kMaxChunk ? oxs::kUnionBig : oxs::kUnionMax) *
+      sizeof(uint64_t);
   const size_t b_theta = B * W * sizeof(uint64_t);
   const size_t b_count = B * W * sizeof(uint32_t);
   bool ok = hipMalloc((void**)&s->lists, b_lists) == hipSuccess &&
