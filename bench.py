@@ -23,6 +23,7 @@ Two secondary measurements print their own JSON line instead:
                        copy of the whole logits to the host;
   --workload dfa_mask  grammar masks (oxs_dfa_mask) for 128 rows over a
                        128256-token vocabulary;
+  --workload configs   oxs_sample_batch on each of the five BASELINE configs;
   --workload lm_head   the Q8_0 LM head that produces the logits (64 columns x
                        128256 tokens x hidden 4096), and the chain quantize ->
                        LM head -> sampler of one decode step.
@@ -362,7 +363,7 @@ def bench_lm_head(args, torch):
     from oxide_sampler import BatchSampler, LmHeadQ8_0, _abi, quantize_q8_1  # noqa: PLC0415
     from oxide_sampler import workloads as wl  # noqa: PLC0415
 
-    m, k, B = 128256, 4096, 64
+    m, k, B = 128256, 4096, args.lm_batch
     nb = k // 32
     rng = np.random.default_rng(0x5EED0011)
     blocks = np.empty((m, nb, 34), np.uint8)
@@ -429,7 +430,7 @@ def bench_lm_head(args, torch):
     alg = m * nb * 34 + B * nb * 36 + B * m * 4
     achieved = alg / (med * 1e-6) / 1e9
     result = {
-        "metric": "Q8_0 LM head logits/s (batch 64 x vocab 128256 x hidden 4096), bit-exact with launch_cuda_mmvq_q8_0",
+        "metric": f"Q8_0 LM head logits/s (batch {B} x vocab 128256 x hidden 4096), bit-exact with launch_cuda_mmvq_q8_0",
         "value": B * m / (med * 1e-6),
         "unit": "logits/s",
         "higher_is_better": True,
@@ -438,18 +439,18 @@ def bench_lm_head(args, torch):
         "median_us_per_step": med,
         "dtype": "int8 x int8 -> i32 (MFMA), f32 accumulation in the reference's order",
         "data": "synthetic Q8_0 weights (uniform int8 quants, f16 scales in [0.002, 0.05]), hidden ~ N(0, 1.5)",
-        "config": {"workload": "lm_head: oxs_mmvq_q8_0, m=128256, k=4096, batch=64 (config 2's decode batch); "
+        "config": {"workload": f"lm_head: oxs_mmvq_q8_0, m=128256, k=4096, batch={B} (64: config 2's decode batch); "
                                "chain = oxs_quantize_q8_1 + oxs_mmvq_q8_0 + oxs_sample_batch (config-2 chain)",
                    "m": m, "k": k, "batch": B, "launch": "hip_graph"},
         "chain_us_per_step": float(np.median(chain_us)),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": alg,
                      "kernel": "mmvq_q8_0_kernel",
-                     "note": "VALU-bound: the reference's float order costs 64 VALU instructions per "
-                             "(32 tokens x 32 columns x k block) beside one MFMA"},
+                     "note": "batch >= 5: MFMA kernel, VALU-bound (48 VALU instructions per 32 tokens x 32 "
+                             "columns x k block beside one MFMA); batch <= 4: dot4 kernel, HBM-bound"},
     }
     tpath = ROOT / "profiles" / "lm_head_pmc_traffic.json"
-    if tpath.exists():
+    if tpath.exists() and B == 64:  # the committed counters were taken at batch 64
         t = json.loads(tpath.read_text())
         result["roofline"]["traffic"] = t["traffic_bytes_per_launch"]
         result["roofline"]["traffic_source"] = str(tpath.relative_to(ROOT))
@@ -457,7 +458,7 @@ def bench_lm_head(args, torch):
         sys.path.insert(0, str(ROOT / "oracle"))
         import oxs_oracle_ctypes as oracle  # noqa: PLC0415 — baseline leg only
 
-        rows = 512  # a bounded sample: 512 token rows x all 64 columns
+        rows = 512  # a bounded sample: 512 token rows x every column
         sub = w_host[: rows * nb * 34]
         xq_host = oracle.quantize_q8_1_host(x.cpu().numpy())
         t0 = time.perf_counter()
@@ -469,7 +470,82 @@ def bench_lm_head(args, torch):
         assert np.array_equal(want.view(np.uint32), y_eager[:, :rows].cpu().numpy().view(np.uint32)), \
             "the GPU logits differ from the oracle's"
         result["cpu_baseline"] = {"value": done * rows * B / dt, "unit": "logits/s", "cores": 1, "kind": "port",
-                                  "sample": f"{done} passes of the first {rows} tokens x 64 columns"}
+                                  "sample": f"{done} passes of the first {rows} tokens x {B} columns"}
+    print(json.dumps(result), flush=True)
+
+
+def bench_configs(args, torch):
+    """oxs_sample_batch on each of BASELINE.json's five configs (graph replays of
+    10 calls over resident inputs): us per call, rows/s and algorithmic GB/s."""
+    from oxide_sampler import BatchSampler  # noqa: PLC0415
+    from oxide_sampler import workloads as wl  # noqa: PLC0415
+
+    d = torch.device("cuda")
+    lines = {}
+    for name, w in (("config1", wl.config1()), ("config2", wl.config2()), ("config3", wl.config3()),
+                    ("config4", wl.config4()), ("config5", wl.config5())):
+        cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
+        sampler = BatchSampler(w.batch, w.vocab, 256)
+        if w.dtype == "bf16":
+            logits = torch.from_numpy(w.logits.view(np.int16)).to(d).view(torch.bfloat16)
+        else:
+            logits = torch.from_numpy(w.logits).to(d)
+        hist = torch.from_numpy(w.history.view(np.int32).copy()).to(d)
+        hlen = torch.from_numpy(w.history_len.view(np.int32).copy()).to(d)
+        mu = torch.from_numpy(w.mu.copy()).to(d) if w.mu is not None else None
+        mask = torch.from_numpy(w.mask.view(np.int32)).to(d) if w.mask is not None else None
+        dcfg = torch.from_numpy(cfg).to(d)
+        u = torch.from_numpy(w.uniforms).to(d)
+        out = {k: torch.empty(w.batch, dtype=torch.int32, device=d) for k in ("tokens", "status", "kept_count")}
+        stream = torch.cuda.Stream()
+
+        def call():
+            sampler.sample(logits, dcfg, mask=mask, history=hist, history_len=hlen, history_cap=0, record=False,
+                           uniforms=u, mirostat_mu=mu, stream=stream, out=out)
+
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                call()
+        torch.cuda.synchronize()
+        assert (out["status"] == 0).all().item(), f"{name}: a row reported a non-OK status"
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(10):
+                call()
+        reps = max(5, args.steps // 400)
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        with torch.cuda.stream(stream):
+            evs[0].record(stream)
+            for i in range(reps):
+                graph.replay()
+                evs[i + 1].record(stream)
+        torch.cuda.synchronize()
+        us = float(np.median([evs[i].elapsed_time(evs[i + 1]) * 1e3 / 10 for i in range(reps)]))
+        H = int(w.history_len[0])
+        esz = 2 if w.dtype == "bf16" else 4
+        words = (w.vocab + 31) // 32 if w.mask is not None else 0
+        alg = algorithmic_bytes(w.batch, w.vocab, H, 0.0, esz=esz, mask_words=words)
+        lines[name] = {"batch": w.batch, "vocab": w.vocab, "dtype": w.dtype, "us_per_call": us,
+                       "rows_per_s": w.batch / (us * 1e-6), "algorithmic_bytes": alg,
+                       "achieved_GBps": alg / (us * 1e-6) / 1e9, "frac": alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                       # one input batch replayed: under 256 MiB it stays in the Infinity Cache
+                       "inputs": "cache-resident" if alg < (256 << 20) else "streamed from HBM"}
+        sampler.close()
+    result = {
+        "metric": "oxs_sample_batch per BASELINE config (config 5: one of its 8 steps)",
+        "value": lines["config2"]["rows_per_s"],
+        "unit": "rows/s",
+        "higher_is_better": True,
+        "n_gpus": 1,
+        "dtype": "f32 / bf16 (config 4)",
+        "data": "synthetic, the seeded workloads of oxide_sampler.workloads",
+        "config": {"workload": "configs: configs 1-5 of BASELINE.json, each as 10 graph-replayed calls"},
+        "configs": lines,
+    }
     print(json.dumps(result), flush=True)
 
 
@@ -570,8 +646,10 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only 8 plain 256 MiB device copies (scale for the rocprofv3 byte counters)")
     ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
-    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head"), default="sample",
-                    help="sample: the headline config-2 line; decode / dfa_mask / lm_head: secondary measurements")
+    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head", "configs"), default="sample",
+                    help="sample: the headline config-2 line; decode / dfa_mask / lm_head / configs: secondary lines")
+    ap.add_argument("--lm-batch", type=int, default=64,
+                    help="lm_head: q8_1 columns (64 = config 2's decode batch; 1 = the last prompt token)")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="turn four rocprofv3 --pmc output folders into the traffic summary and exit")
     ap.add_argument("--trace-summary", default=str(ROOT / "profiles" / "config2_kernel_trace.json"))
@@ -611,6 +689,9 @@ def main():
         return
     if args.workload == "lm_head":
         bench_lm_head(args, torch)
+        return
+    if args.workload == "configs":
+        bench_configs(args, torch)
         return
     if args.calibrate_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device=d)  # 256 MiB
