@@ -148,7 +148,7 @@ def bench_decode(args, torch):
     B, V = w.batch, w.vocab
     H = int(w.history_len[0])
     n = max(50, args.steps)
-    pool = make_pool(torch, w, 4)
+    pool = make_pool(torch, w, pool_batches(B * V * 4))
     loop = DecodeLoop(B, V, history_cap=H + 3 * n + 64)
     for slot in range(B):
         st = SamplerState(10.0, w.history[slot, :H].tolist())
@@ -210,9 +210,10 @@ def bench_decode(args, torch):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     g_arg = torch.cuda.CUDAGraph()
+    n_arg = 3 * len(pool)  # a rotation over the whole pool: read from HBM
     with torch.cuda.graph(g_arg, stream=side):
-        for _ in range(50):
-            lib.oxs_argmax(ctypes.c_void_p(pool[0].data_ptr()), V, V, B, ctypes.c_void_p(tok.data_ptr()),
+        for i in range(n_arg):
+            lib.oxs_argmax(ctypes.c_void_p(pool[i % len(pool)].data_ptr()), V, V, B, ctypes.c_void_p(tok.data_ptr()),
                            ctypes.c_void_p(val.data_ptr()), ctypes.c_void_p(side.cuda_stream))
     g_arg.replay()
     torch.cuda.synchronize()
@@ -222,7 +223,7 @@ def bench_decode(args, torch):
         g_arg.replay()
     e1.record()
     torch.cuda.synchronize()
-    argmax_us = e0.elapsed_time(e1) * 1e3 / (20 * 50)
+    argmax_us = e0.elapsed_time(e1) * 1e3 / (20 * n_arg)
     # the reference's hand-off: the whole logits to pinned host memory
     # (oxide-backend-cuda/src/lib.rs:6037-6041), before any CPU sampling
     host = torch.empty(B, V, dtype=torch.float32, pin_memory=True)
@@ -241,10 +242,12 @@ def bench_decode(args, torch):
         "n_gpus": 1,
         "steps": n,
         "dtype": "f32",
-        "data": "synthetic (config-2 batch and 3 GPU-drawn batches of the same distribution)",
+        "data": f"synthetic (config-2 batch and {len(pool) - 1} GPU-drawn batches of the same distribution)",
         "config": {"workload": "decode: 64 sequences, config-2 SamplingConfig and a 512-token history each, "
                                "device xorshift draws; DecodeLoop over oxs_decode_step"},
         "graph_replay_us": _percentiles(t_graph),
+        "graph_replay_inputs": "one captured batch, replayed: cache-resident (32.8 MB < 256 MiB Infinity Cache)",
+        "pool_bytes": len(pool) * B * V * 4,
         "eager_launch_us": _percentiles(t_eager),
         "gpu_us_per_step": gpu_us,
         "sample_then_copy_tokens_us": _percentiles(t_copy),
@@ -474,46 +477,118 @@ def bench_lm_head(args, torch):
     print(json.dumps(result), flush=True)
 
 
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def pool_batches(batch_bytes, at_least=2):
+    """Distinct input batches whose total exceeds twice the Infinity Cache, so
+    a rotation over them streams from HBM."""
+    return max(at_least, (2 * MALL_BYTES) // batch_bytes + 1)
+
+
+def config_pool(torch, w, n_pool, seed):
+    """[n_pool, B, V] logits for workload w: entry 0 is the seeded CPU workload,
+    the rest are drawn on the GPU from the same distribution
+    (oxide_sampler.workloads: config 1 N(0,2) + 5 spikes at +8; configs 2-3
+    N(0,3) + -1.1 ln(rank) over a random permutation; config 4 N(0,2.5) with 1%
+    of entries U[6,10], as bf16; config 5 N(0,2))."""
+    d = torch.device("cuda")
+    B, V = w.batch, w.vocab
+    g = torch.Generator(device=d)
+    g.manual_seed(seed)
+    dt = torch.bfloat16 if w.dtype == "bf16" else torch.float32
+    pool = torch.empty(n_pool, B, V, dtype=dt, device=d)
+    if w.dtype == "bf16":
+        pool[0] = torch.from_numpy(w.logits.view(np.int16)).to(d).view(torch.bfloat16)
+    else:
+        pool[0] = torch.from_numpy(w.logits).to(d)
+    prior = (-1.1 * torch.log(torch.arange(1, V + 1, device=d, dtype=torch.float64))).to(torch.float32)
+    for i in range(1, n_pool):
+        if w.name == "config1":
+            x = torch.randn(B, V, device=d, generator=g) * 2.0
+            spikes = torch.randint(0, V, (B, 5), device=d, generator=g)
+            x.scatter_(1, spikes, 8.0)
+        elif w.name in ("config2", "config3"):
+            x = torch.randn(B, V, device=d, generator=g) * 3.0
+            x += prior[torch.argsort(torch.rand(B, V, device=d, generator=g), dim=1)]
+        elif w.name == "config4":
+            x = torch.randn(B, V, device=d, generator=g) * 2.5
+            heavy = torch.rand(B, V, device=d, generator=g) < 0.01
+            x = torch.where(heavy, 6.0 + 4.0 * torch.rand(B, V, device=d, generator=g), x)
+        else:
+            x = torch.randn(B, V, device=d, generator=g) * 2.0
+        pool[i] = x.to(dt)
+    return pool
+
+
+def config_masks(torch, w, n_pool, seed):
+    """[n_pool, B, ceil(V/32)] packed masks for config 3: entry 0 the seeded one,
+    the rest with each bit set with probability 0.03 and one guaranteed id."""
+    d = torch.device("cuda")
+    B, V = w.batch, w.vocab
+    words = (V + 31) // 32
+    g = torch.Generator(device=d)
+    g.manual_seed(seed)
+    out = torch.empty(n_pool, B, words, dtype=torch.int32, device=d)
+    out[0] = torch.from_numpy(w.mask.view(np.int32)).to(d)
+    weights = (2 ** torch.arange(32, device=d, dtype=torch.int64))
+    for i in range(1, n_pool):
+        bits = torch.rand(B, words * 32, device=d, generator=g) < 0.03
+        bits[:, V:] = False
+        bits[torch.arange(B, device=d), torch.randint(0, V, (B,), device=d, generator=g)] = True
+        packed = (bits.view(B, words, 32).to(torch.int64) * weights).sum(-1)
+        out[i] = packed.to(torch.uint32).view(torch.int32) if hasattr(torch, "uint32") else \
+            ((packed + 2**31) % 2**32 - 2**31).to(torch.int32)
+    return out
+
+
 def bench_configs(args, torch):
-    """oxs_sample_batch on each of BASELINE.json's five configs (graph replays of
-    10 calls over resident inputs): us per call, rows/s and algorithmic GB/s."""
+    """oxs_sample_batch on each of BASELINE.json's five configs. Each config
+    rotates over its own pool of distinct input batches larger than twice the
+    Infinity Cache (graph replays of the whole rotation), so every figure is
+    streamed from HBM: us per call, rows/s, algorithmic GB/s with its roofline
+    fraction, and how each row's top M was found (path counters)."""
     from oxide_sampler import BatchSampler  # noqa: PLC0415
     from oxide_sampler import workloads as wl  # noqa: PLC0415
 
     d = torch.device("cuda")
     lines = {}
-    for name, w in (("config1", wl.config1()), ("config2", wl.config2()), ("config3", wl.config3()),
-                    ("config4", wl.config4()), ("config5", wl.config5())):
+    for cfg_id in (1, 2, 3, 4, 5):
+        w = wl.BUILDERS[cfg_id]()
+        name = w.name
         cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
         sampler = BatchSampler(w.batch, w.vocab, 256)
-        if w.dtype == "bf16":
-            logits = torch.from_numpy(w.logits.view(np.int16)).to(d).view(torch.bfloat16)
-        else:
-            logits = torch.from_numpy(w.logits).to(d)
+        esz = 2 if w.dtype == "bf16" else 4
+        words = (w.vocab + 31) // 32 if w.mask is not None else 0
+        batch_bytes = w.batch * (w.vocab * esz + words * 4)
+        P = pool_batches(batch_bytes)
+        pool = config_pool(torch, w, P, 0x5EED0100 + cfg_id)
+        masks = config_masks(torch, w, P, 0x5EED0200 + cfg_id) if w.mask is not None else None
         hist = torch.from_numpy(w.history.view(np.int32).copy()).to(d)
         hlen = torch.from_numpy(w.history_len.view(np.int32).copy()).to(d)
         mu = torch.from_numpy(w.mu.copy()).to(d) if w.mu is not None else None
-        mask = torch.from_numpy(w.mask.view(np.int32)).to(d) if w.mask is not None else None
         dcfg = torch.from_numpy(cfg).to(d)
         u = torch.from_numpy(w.uniforms).to(d)
         out = {k: torch.empty(w.batch, dtype=torch.int32, device=d) for k in ("tokens", "status", "kept_count")}
         stream = torch.cuda.Stream()
 
-        def call():
-            sampler.sample(logits, dcfg, mask=mask, history=hist, history_len=hlen, history_cap=0, record=False,
-                           uniforms=u, mirostat_mu=mu, stream=stream, out=out)
+        def call(i):
+            sampler.sample(pool[i], dcfg, mask=None if masks is None else masks[i], history=hist, history_len=hlen,
+                           history_cap=0, record=False, uniforms=u, mirostat_mu=mu, stream=stream, out=out)
 
         stream.wait_stream(torch.cuda.current_stream())
+        sampler.count_paths(True)
         with torch.cuda.stream(stream):
-            for _ in range(3):
-                call()
+            call(0)
         torch.cuda.synchronize()
+        paths = sampler.path_counts()
+        sampler.count_paths(False)
         assert (out["status"] == 0).all().item(), f"{name}: a row reported a non-OK status"
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
-            for _ in range(10):
-                call()
-        reps = max(5, args.steps // 400)
+            for i in range(P):
+                call(i)
+        reps = max(3, min(50, 4000 // P))
         with torch.cuda.stream(stream):
             graph.replay()
         torch.cuda.synchronize()
@@ -524,17 +599,20 @@ def bench_configs(args, torch):
                 graph.replay()
                 evs[i + 1].record(stream)
         torch.cuda.synchronize()
-        us = float(np.median([evs[i].elapsed_time(evs[i + 1]) * 1e3 / 10 for i in range(reps)]))
+        us = float(np.median([evs[i].elapsed_time(evs[i + 1]) * 1e3 / P for i in range(reps)]))
         H = int(w.history_len[0])
-        esz = 2 if w.dtype == "bf16" else 4
-        words = (w.vocab + 31) // 32 if w.mask is not None else 0
         alg = algorithmic_bytes(w.batch, w.vocab, H, 0.0, esz=esz, mask_words=words)
+        gbs = alg / (us * 1e-6) / 1e9
         lines[name] = {"batch": w.batch, "vocab": w.vocab, "dtype": w.dtype, "us_per_call": us,
                        "rows_per_s": w.batch / (us * 1e-6), "algorithmic_bytes": alg,
-                       "achieved_GBps": alg / (us * 1e-6) / 1e9, "frac": alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                       # one input batch replayed: under 256 MiB it stays in the Infinity Cache
-                       "inputs": "cache-resident" if alg < (256 << 20) else "streamed from HBM"}
+                       "pool_batches": P, "pool_bytes": P * batch_bytes,
+                       "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                    "frac": gbs / HBM_PEAK_GBS},
+                       "top_m_paths": paths}
+        print(f"[configs] {name}: {us:.2f} us per call, {gbs:.0f} GB/s, paths {paths}", file=sys.stderr, flush=True)
         sampler.close()
+        del pool, masks
+        torch.cuda.empty_cache()
     result = {
         "metric": "oxs_sample_batch per BASELINE config (config 5: one of its 8 steps)",
         "value": lines["config2"]["rows_per_s"],
@@ -542,8 +620,10 @@ def bench_configs(args, torch):
         "higher_is_better": True,
         "n_gpus": 1,
         "dtype": "f32 / bf16 (config 4)",
-        "data": "synthetic, the seeded workloads of oxide_sampler.workloads",
-        "config": {"workload": "configs: configs 1-5 of BASELINE.json, each as 10 graph-replayed calls"},
+        "data": "synthetic: the seeded workloads of oxide_sampler.workloads plus GPU-drawn batches of each "
+                "config's distribution",
+        "config": {"workload": "configs: configs 1-5 of BASELINE.json, each rotating over more than 512 MiB "
+                               "of distinct input batches"},
         "configs": lines,
     }
     print(json.dumps(result), flush=True)
@@ -621,9 +701,10 @@ def summarize_trace(folder):
     out = {}
     for r in csv.DictReader(open(stats)):
         name = r["Name"]
-        for k in ("stream_kernel", "tail_kernel"):
-            if f"oxs::{k}<" in name and "<0" in name[name.index(k):name.index(k) + len(k) + 3]:
-                out[k] = {"avg_ns": float(r["AverageNs"]), "calls": int(r["Calls"]), "name": name}
+        if "oxs::sample_kernel<0," in name:  # the f32 kernels (config 2)
+            prev = out.get("sample_kernel")
+            if prev is None or int(r["Calls"]) > prev["calls"]:
+                out["sample_kernel"] = {"avg_ns": float(r["AverageNs"]), "calls": int(r["Calls"]), "name": name}
     return out
 
 
@@ -639,7 +720,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=8000)
     ap.add_argument("--warmup", type=int, default=800)
-    ap.add_argument("--pool", type=int, default=16, help="distinct input batches (16 x 32.8 MB > 2 x 256 MiB)")
+    ap.add_argument("--pool", type=int, default=0,
+                    help="distinct input batches; 0 = enough to exceed 2 x 256 MiB (17 x 32.8 MB = 533 MiB)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch from a Python loop instead of a HIP graph")
@@ -704,7 +786,7 @@ def main():
     w = wl.config2()
     B, V = w.batch, w.vocab
     H = int(w.history_len[0])
-    pool = make_pool(torch, w, args.pool)
+    pool = make_pool(torch, w, args.pool or pool_batches(B * V * 4))
     cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
     d_cfg = torch.from_numpy(cfg).to(d)
     d_hist = torch.from_numpy(w.history.view(np.int32).copy()).to(d)
@@ -822,7 +904,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded config-2 batch + 15 GPU-drawn batches of the same distribution)",
+        "data": f"synthetic (seeded config-2 batch + {P - 1} GPU-drawn batches of the same distribution)",
         "config": {
             "workload": "config2: B=64 x V=128256 f32 logits, history 512; freq 0.3 + presence 0.2 + repeat 1.05 "
                         "-> temp 0.7 -> top-k 50 -> top-p 0.9 -> min-p 0.05 -> draw with supplied u",
@@ -841,24 +923,18 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes_per_launch": alg,
             "traffic_source": traffic_src,
-            "kernel": "oxs_sample_batch = stream_kernel + tail_kernel (one launch pair, timed together)",
+            "kernel": "oxs_sample_batch = one sample_kernel launch (stream phase + each row's tail in its "
+                      "last-arriving block), timed with HIP events on its launch stream",
         },
         "wall_s": wall,
     }
-    # The call is two kernels: the HBM-bound stream kernel moves the logits
-    # (everything but the tail's candidate lists and outputs); the tail is
-    # latency-bound. Their split, from the committed kernel trace of this bench.
+    # The same kernel's average duration from the committed rocprofv3 kernel
+    # trace of this bench (it must agree with the events above).
     split, split_src = read_kernel_trace(args.trace_summary)
-    if split and "stream_kernel" in split:
-        stream_bytes = B * (V * 4 + H * 4 + 104)
-        sk = split["stream_kernel"]["avg_ns"] * 1e-9
-        per = {"stream_kernel": {"avg_us": sk * 1e6, "algorithmic_bytes": stream_bytes,
-                                 "achieved": stream_bytes / sk / 1e9, "frac": stream_bytes / sk / 1e9 / HBM_PEAK_GBS,
-                                 "bound": "hbm"}}
-        if "tail_kernel" in split:
-            per["tail_kernel"] = {"avg_us": split["tail_kernel"]["avg_ns"] * 1e-3, "bound": "latency"}
-        result["roofline"]["per_kernel"] = per
-        result["roofline"]["per_kernel_source"] = split_src
+    if split and "sample_kernel" in split:
+        sk = split["sample_kernel"]["avg_ns"] * 1e-9
+        result["roofline"]["trace_check"] = {"sample_kernel_avg_us": sk * 1e6, "achieved": alg / sk / 1e9,
+                                             "frac": alg / sk / 1e9 / HBM_PEAK_GBS, "source": split_src}
     if achieved > 1.05 * HBM_PEAK_GBS:  # roofline.rs:53-style integrity check
         result["roofline"]["warning"] = "achieved exceeds 1.05 x peak: inputs were cached, not streamed"
     if not args.no_cpu:

@@ -205,6 +205,26 @@ int oxs_sampler_destroy(oxs_sampler* sampler);
 size_t oxs_sampler_workspace_bytes(const oxs_sampler* sampler);
 
 /*
+ * Diagnostics, no counterpart in the reference: per-row counts of how each
+ * row's top M = max(top_k, 256) candidates were found, for tests and tuning.
+ * counts[OXS_PATH_BUCKETS]: a bucketed counting sort of the stream phase's
+ * candidate keys (the fast path); [OXS_PATH_SORT]: a bitonic sort of those
+ * keys (a bucket held too many); [OXS_PATH_EXACT]: a radix select over the
+ * whole row (the candidates could not be proven to hold the top M, or the
+ * row uses DRY); [OXS_PATH_NONE]: the row ended before the selection
+ * (OXS_ROW_UNSUPPORTED, OXS_ROW_MISSING_STATE).
+ * oxs_sampler_count_paths turns the counting on (enable != 0) or off for later
+ * calls and zeroes the counts; oxs_sampler_path_counts copies them out. Both
+ * synchronise the device: not for the decode loop.
+ */
+#define OXS_PATH_BUCKETS 0
+#define OXS_PATH_SORT 1
+#define OXS_PATH_EXACT 2
+#define OXS_PATH_NONE 3
+int oxs_sampler_count_paths(oxs_sampler* sampler, int enable);
+int oxs_sampler_path_counts(const oxs_sampler* sampler, uint32_t counts[4]);
+
+/*
  * Samples every row of `batch` on `stream` (a hipStream_t; NULL = default
  * stream). Replaces B serial calls of
  *   AcademicSamplerEngine::sample_token(&self, logits: &mut [f32],

@@ -39,6 +39,11 @@ OXS_DTYPE_BF16 = 1
 OXS_FLAG_RECORD_HISTORY = 1
 OXS_FLAG_SHARED_CONFIG = 2
 
+OXS_PATH_BUCKETS = 0
+OXS_PATH_SORT = 1
+OXS_PATH_EXACT = 2
+OXS_PATH_NONE = 3
+
 # Exported symbols declared in include/oxide_sampler.h.
 EXPORTED_SYMBOLS = (
     "oxs_abi_version",
@@ -49,6 +54,8 @@ EXPORTED_SYMBOLS = (
     "oxs_sampler_create",
     "oxs_sampler_destroy",
     "oxs_sampler_workspace_bytes",
+    "oxs_sampler_count_paths",
+    "oxs_sampler_path_counts",
     "oxs_sample_batch",
     "oxs_decode_step",
     "oxs_argmax",
@@ -209,6 +216,10 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_sampler_destroy.argtypes = [ctypes.c_void_p]
     lib.oxs_sampler_workspace_bytes.restype = ctypes.c_size_t
     lib.oxs_sampler_workspace_bytes.argtypes = [ctypes.c_void_p]
+    lib.oxs_sampler_count_paths.restype = ctypes.c_int
+    lib.oxs_sampler_count_paths.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    lib.oxs_sampler_path_counts.restype = ctypes.c_int
+    lib.oxs_sampler_path_counts.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]
     lib.oxs_sample_batch.restype = ctypes.c_int
     lib.oxs_sample_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.c_void_p]
     lib.oxs_decode_step.restype = ctypes.c_int

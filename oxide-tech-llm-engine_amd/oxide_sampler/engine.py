@@ -192,6 +192,16 @@ class BatchSampler:
     def workspace_bytes(self) -> int:
         return int(self.lib.oxs_sampler_workspace_bytes(self.handle))
 
+    def count_paths(self, enable: bool = True) -> None:
+        """Turns the per-row top-M path counters on or off and zeroes them (synchronises)."""
+        check(self.lib.oxs_sampler_count_paths(self.handle, 1 if enable else 0), "oxs_sampler_count_paths")
+
+    def path_counts(self) -> dict:
+        """Rows per top-M selection path since the counters were zeroed: buckets, sort, exact, none."""
+        c = (ctypes.c_uint32 * 4)()
+        check(self.lib.oxs_sampler_path_counts(self.handle, c), "oxs_sampler_path_counts")
+        return {"buckets": int(c[0]), "sort": int(c[1]), "exact": int(c[2]), "none": int(c[3])}
+
     def launch(self, batch: OxsBatch, stream=None, decode: Optional[OxsDecodeIo] = None) -> None:
         """Raw launch of a prepared descriptor on `stream` (torch stream or None);
         with `decode`, a decode step (oxs_decode_step)."""

@@ -59,21 +59,50 @@ def test_config4_full(torch_gpu):
     compare(run_gpu(w, torch_gpu), run_oracle(w), RTOL_BF16, "config4")
 
 
-def test_config5_eight_steps(torch_gpu):
-    w = wl.config5(batch=64)
-    banner("config5 B=64 V=262144 mirostat v2 x8 steps")
+def oracle_threads():
+    """Host threads for the oracle: the GPU box's CPU share is 16 cores, whatever os.cpu_count() shows."""
+    import os
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+@pytest.mark.parametrize("batch", [64, 512])
+def test_config5_eight_steps(torch_gpu, batch):
+    # batch 512 is config 5 itself: B=512 x V=262144 (537 MB of logits per step, rows grouped
+    # 64 per XCD, 16384 stream blocks); batch 64 is the smaller grouping (8 rows per XCD)
+    w = wl.config5(batch=batch)
+    nt = oracle_threads()
     g_hist, g_len, g_mu = w.history.copy(), w.history_len.copy(), w.mu.copy()
     r_hist, r_len, r_mu = w.history.copy(), w.history_len.copy(), w.mu.copy()
     for step in range(w.steps):
+        banner(f"config5 B={batch} V=262144 mirostat v2 step {step} (oracle on {nt} threads)")
         w.logits = wl.config5_step_logits(w.batch, w.vocab, wl.SEED_BASE + 5, step)
         w.history, w.history_len, w.mu = g_hist, g_len, g_mu
         g = run_gpu(w, torch_gpu)
         w.history, w.history_len, w.mu = r_hist, r_len, r_mu
-        r = run_oracle(w)
-        compare(g, r, RTOL_F32, f"config5 step {step}")
+        r = run_oracle(w, n_threads=nt)
+        compare(g, r, RTOL_F32, f"config5 B={batch} step {step}")
         g_hist, g_len, g_mu = g.history, g.history_len, g.mu
         r_hist, r_len, r_mu = r.history, r.history_len, r.mu
-    assert int(r_len[0]) == 256 + 2 * w.steps  # two records per Mirostat step (sampler.rs:301, :307)
+    assert (r_len == 256 + 2 * w.steps).all()  # two records per Mirostat step (sampler.rs:301, :307)
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_baseline_configs_take_the_candidate_path(torch_gpu, cfg):
+    # the exact re-scan gives the same answers (parity cannot see it) at many times the cost:
+    # every row of a BASELINE config must find its top M among the stream phase's candidates
+    from harness import gpu_sampler
+    w = wl.BUILDERS[cfg]()
+    banner(f"config{cfg} B={w.batch} V={w.vocab}: top-M selection paths")
+    s = gpu_sampler(w.batch, w.vocab)
+    s.count_paths(True)
+    try:
+        run_gpu(w, torch_gpu)
+        counts = s.path_counts()
+    finally:
+        s.count_paths(False)
+    print(f"config{cfg} paths: {counts}", flush=True)
+    assert counts["exact"] == 0 and counts["none"] == 0, counts
+    assert counts["buckets"] + counts["sort"] == w.batch, counts
 
 
 def mixed_workload(B, V, seed):
@@ -123,8 +152,9 @@ def mixed_workload(B, V, seed):
                        history_len=hlen, uniforms=wl.xorshift_uniforms(B, seed), mu=mu)
 
 
-@pytest.mark.parametrize("V", [1, 3, 257, 4097, 50001, 131072])
+@pytest.mark.parametrize("V", [1, 3, 257, 4097, 50001, 131072, 151936, 262144])
 def test_mixed_configs_ragged_vocab(torch_gpu, V):
+    # B = 40 groups rows by XCD (5 per XCD); vocabularies past 131072 take the 4096-key union
     B = 40 if V >= 4097 else 12
     w = mixed_workload(B, V, seed=100 + V)
     banner(f"mixed configs B={B} V={V}")

@@ -6,8 +6,9 @@ grammar mask (none, per row or shared), a softcap, histories of random
 length, and for every row a SamplingConfig whose fields are each enabled with
 probability 1/2 at random values (sampler.rs:16-73). The HIP path must match
 the oracle exactly: tokens, status, kept ids and probabilities, history, mu.
-Rows the device declines (top_k > 1024, DRY slices > 1024) report
-OXS_ROW_UNSUPPORTED in both.
+`test_random_configs_large_vocab` draws vocabularies above 131072 (more than 16
+stream chunks per row, the 4096-key candidate union) with batches divisible by 8
+(rows grouped by XCD).
 """
 import numpy as np
 import pytest
@@ -68,10 +69,14 @@ def random_config(rng, V):
     return wl.disabled_config(**kw)
 
 
-def random_workload(seed):
+def random_workload(seed, large_vocab=False):
     rng = np.random.default_rng(seed)
-    B = int(rng.choice([1, 3, 8, 17, 33]))
-    V = int(rng.choice([5, 100, 1000, 4097, 20000, 65537]))
+    if large_vocab:
+        B = int(rng.choice([8, 16, 24, 40]))
+        V = int(rng.choice([151936, 262144]))
+    else:
+        B = int(rng.choice([1, 3, 8, 17, 33]))
+        V = int(rng.choice([5, 100, 1000, 4097, 20000, 65537]))
     kind = rng.integers(0, 3)
     x = rng.standard_normal((B, V)).astype(np.float32) * np.float32(rng.choice([0.5, 2.0, 4.0]))
     if kind == 1:  # a heavy tail of spikes
@@ -114,6 +119,17 @@ def test_random_configs(torch_gpu, seed):
            f"softcap={w.extra.get('softcap', 0)}")
     g = run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=1024, shared_mask=shared)
     r = run_oracle(w, kept_ld=1024, logits_out=True, shared_mask=shared)
+    compare(g, r, RTOL_BF16 if w.dtype == "bf16" else RTOL_F32, w.name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(8))
+def test_random_configs_large_vocab(torch_gpu, seed):
+    w, shared = random_workload(2000 + seed, large_vocab=True)
+    banner(f"{w.name} {w.dtype} mask={'shared' if shared else w.mask is not None} "
+           f"softcap={w.extra.get('softcap', 0)}")
+    g = run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=1024, shared_mask=shared)
+    r = run_oracle(w, kept_ld=1024, logits_out=True, shared_mask=shared, n_threads=8)
     compare(g, r, RTOL_BF16 if w.dtype == "bf16" else RTOL_F32, w.name)
 
 
