@@ -43,6 +43,7 @@ constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / 64;
 constexpr int kUnionMax = 2048;   // candidate key slots per row
 constexpr int kUnionBig = 4096;   // ... for rows of more than 64 wavefront records (V > 16 chunks)
+constexpr int kTailArea = 4096;   // 64-bit words of tail LDS shared by the scatter, sort, exact-path table and chain scratch
 constexpr int kMaxM = 1024;       // largest max(top_k, 256) run on the device
 constexpr int kMaxChunk = 8192;   // logits per stream block
 constexpr int kMaxChunks = 64;    // chunks per row
@@ -51,8 +52,6 @@ constexpr int kRecPer = kMaxChunks * kWavesPerBlock / 64;  // wavefront records 
 constexpr int kDryMax = 1024;      // longest DRY history slice run on the device (sampler.rs:395)
 constexpr int kDryHash = 2048;     // DRY id hash slots
 constexpr int kHistUnroll = 4;    // history-window ids per stream thread read with the logits
-constexpr int kTableMax = 4096;   // ids per piece of the exact path's LDS penalty table
-constexpr int kTicketStride = 16; // uint32 words between rows' arrival counters (64 bytes)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -67,8 +66,10 @@ constexpr uint32_t kFlagDecode = 1u << 31;  // Params.flags: a decode step (oxs_
 // compile-time features, so that launches without a feature carry none of its
 // code.
 constexpr int kKindSoftcap = 4;  // logits pass through the softcap as they are read
+constexpr int kKindDecode = 8;   // tail only: the decode step's bookkeeping
 constexpr bool kind_f32(int k) { return (k & 3) == OXS_DTYPE_F32; }
 constexpr bool kind_softcap(int k) { return (k & kKindSoftcap) != 0; }
+constexpr bool kind_decode(int k) { return (k & kKindDecode) != 0; }
 
 struct Params {
   const void* logits;
@@ -116,7 +117,6 @@ struct Params {
   uint32_t* dec_count;    // [B] generated count
   uint64_t* host_tokens;  // [B] host memory: (row's step count << 32) | token
   uint32_t* row_steps;    // [B] workspace: decode steps each row has handed to the host
-  uint32_t* tickets;      // [B][kTicketStride] workspace: the row's blocks that finished the stream phase
   uint32_t* path_counts;  // [kPathKinds] workspace, or NULL: rows per top-M selection path
 };
 
@@ -159,11 +159,21 @@ struct RowXf {
   uint32_t bias_off, bias_cnt, ban_off, ban_cnt;
 };
 
-__device__ __forceinline__ RowXf make_row_xf_h(const Params& p, const oxs_sampling_config& c,
-                                               uint32_t hlen) {
+// Which optional inputs a launch has (sample_kernel's and stream_kernel's
+// `kflags`), so that the row setup needs no kernel-argument load.
+constexpr uint32_t kKShared = 1u;   // one config for every row
+constexpr uint32_t kKDecode = 2u;   // a decode step (oxs_decode_step)
+constexpr uint32_t kKHistory = 4u;  // history and history_len are present
+constexpr uint32_t kKBias = 8u;     // bias_ids is present
+constexpr uint32_t kKBan = 16u;     // ban_ids is present
+
+// Per-row constants from the config, the history length (clamped to the
+// history's row stride) and the launch's presence flags.
+__device__ __forceinline__ RowXf make_row_xf(const oxs_sampling_config& c, uint32_t hlen, uint32_t V,
+                                             uint32_t history_ld, uint32_t kflags) {
   RowXf r;
-  if (!(p.history && p.history_len)) hlen = 0u;
-  if ((int64_t)hlen > p.history_ld) hlen = (uint32_t)p.history_ld;
+  if (!(kflags & kKHistory)) hlen = 0u;
+  if (hlen > history_ld) hlen = history_ld;
   r.hlen = hlen;
   r.rp = c.repeat_penalty;
   r.fp = c.frequency_penalty;
@@ -174,13 +184,13 @@ __device__ __forceinline__ RowXf make_row_xf_h(const Params& p, const oxs_sampli
   uint32_t wlen = c.repeat_last_n > 0 ? c.repeat_last_n : hlen;  // :209-213
   r.wstart = hlen > wlen ? hlen - wlen : 0u;
   r.wn = hlen - r.wstart;
-  r.nl_active = c.penalize_nl != 0 && c.newline_token_id < p.V;  // :196-197
+  r.nl_active = c.penalize_nl != 0 && c.newline_token_id < V;  // :196-197
   r.nl_id = c.newline_token_id;
   r.nl_pen = c.newline_penalty;
   r.bias_off = c.bias_offset;
-  r.bias_cnt = p.bias_ids ? c.bias_count : 0u;
+  r.bias_cnt = (kflags & kKBias) ? c.bias_count : 0u;
   r.ban_off = c.ban_offset;
-  r.ban_cnt = p.ban_ids ? c.ban_count : 0u;
+  r.ban_cnt = (kflags & kKBan) ? c.ban_count : 0u;
   r.do_temp = c.temperature > 0.0f && c.mirostat_mode == OXS_MIROSTAT_DISABLED;  // :249
   r.inv_temp = 1.0f / c.temperature;                                               // :250
   r.dry = c.dry_multiplier > 0.0f && hlen > 0;                                     // :203
@@ -190,6 +200,16 @@ __device__ __forceinline__ RowXf make_row_xf_h(const Params& p, const oxs_sampli
   r.dry_range = c.dry_range;
   r.any_special = r.use_hist || r.bias_cnt > 0 || r.ban_cnt > 0 || r.nl_active || r.dry;
   return r;
+}
+
+// The launch's presence flags, from its Params.
+__device__ __forceinline__ uint32_t launch_kflags(const Params& p) {
+  return ((p.flags & OXS_FLAG_SHARED_CONFIG) ? kKShared : 0u) | ((p.flags & kFlagDecode) ? kKDecode : 0u) |
+         ((p.history && p.history_len) ? kKHistory : 0u) | (p.bias_ids ? kKBias : 0u) |
+         (p.ban_ids ? kKBan : 0u);
+}
+__device__ __forceinline__ RowXf make_row_xf_h(const Params& p, const oxs_sampling_config& c, uint32_t hlen) {
+  return make_row_xf(c, hlen, p.V, (uint32_t)p.history_ld, launch_kflags(p));
 }
 
 
@@ -426,25 +446,6 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// The hand-off between a row's blocks. What one block writes for another
-// (candidate keys, wavefront records, write-back logits) is stored through to
-// memory with system-coherent vector stores, and the reading block loads it
-// with system-coherent loads that bypass its caches; the row's arrival counter
-// is a system-scope atomic. This holds wherever the blocks run, whichever XCD
-// (and L2) each one lands on. All of these are vector memory instructions.
-__device__ __forceinline__ void publish_u64(uint64_t* a, uint64_t v) {
-  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ void publish_u32(uint32_t* a, uint32_t v) {
-  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ uint64_t collect_u64(const uint64_t* a) {
-  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ uint32_t collect_u32(const uint32_t* a) {
-  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
 // Exclusive prefix sum over the block; *total gets the block sum.
 __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, uint32_t* scratch) {
   const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -500,19 +501,9 @@ __device__ __forceinline__ uint32_t hash_lookup(const uint32_t* hkeys, const uin
 }
 
 
-// ---------------------------------------------------------------- stream phase
+// ---------------------------------------------------------------- stream kernel
 
 constexpr uint32_t kMinValidOrd = 0x00800000u;  // f2ord(-FLT_MAX): every candidate key is >= this
-
-// LDS of the stream phase: each thread's masked raw logits (private slots,
-// indexed by chunk offset) and the hash of the chunk's sparse-stage ids.
-template <int NE>
-struct StreamLds {
-  float x[NE * kThreads];
-  uint32_t hkeys[kHashSlots];
-  uint32_t hvals[kHashSlots];
-  uint32_t full;
-};
 
 // One unit after its logits arrived. The dense stages (grammar mask, end of
 // vocabulary) are applied in registers and the values are staged in LDS,
@@ -524,16 +515,14 @@ struct StreamLds {
 // (order key of x * inv_temp << 32 | ~token id). Thresholds and comparisons
 // use the unscaled values: x -> x * inv_temp is monotone for a finite positive
 // scale, and a row with any other scale is sent to the tail's exact path.
-// `mw` holds each load group's mask word (all ones without a mask).
-template <int DT, int SLOTS>
+template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
 __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint32_t chunk, const RowXf& r,
                                              const uint32_t (&raw)[SLOTS][kind_f32(DT) ? 4 : 8],
-                                             const uint32_t (&mw)[SLOTS],
-                                             StreamLds<SLOTS * (kind_f32(DT) ? 4 : 8)>& sl) {
+                                             const uint32_t (&mw)[SLOTS], float* s_x, uint32_t* s_hkeys,
+                                             uint32_t* s_hvals, uint32_t* s_full) {
   constexpr int EPL = kind_f32(DT) ? 4 : 8;
   constexpr int TILE = kThreads * EPL;
   constexpr int NE = SLOTS * EPL;
-  float* s_x = sl.x;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t CH = SLOTS * TILE;
   const uint32_t c0 = chunk * CH;
@@ -544,22 +533,23 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
   // ---- masked raw logits, staged in LDS at their chunk offsets
   float v[NE];
 #pragma unroll
-  for (int i = 0; i < NE; ++i) v[i] = __uint_as_float(raw[i / EPL][i % EPL]);
-  if (p.mask) {
+  for (int s = 0; s < SLOTS; ++s) {
+    const uint32_t off = s * TILE + tid * EPL;  // chunk-local
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const uint32_t off = s * TILE + tid * EPL;  // chunk-local
-#pragma unroll
-      for (int e = 0; e < EPL; ++e)
-        if (!((mw[s] >> ((c0 + off + e) & 31)) & 1u)) v[s * EPL + e] = neg_inf();
+    for (int e = 0; e < EPL; ++e) {
+      float x = __uint_as_float(raw[s][e]);
+      if (MASK && !((mw[s] >> ((c0 + off + e) & 31)) & 1u)) x = neg_inf();
+      if (!VEC && c0 + off + e >= c1) x = neg_inf();
+      v[s * EPL + e] = x;
     }
   }
-  if (c1 - c0 < CH) {  // a short last chunk: logits past the end are dropped
+  if (VEC && c1 - c0 < CH) {  // a short last chunk: groups past the end are dropped
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s)
+      if (c0 + s * TILE + tid * EPL >= c1) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e)
-        if (c0 + s * TILE + tid * EPL + e >= c1) v[s * EPL + e] = neg_inf();
+        for (int e = 0; e < EPL; ++e) v[s * EPL + e] = neg_inf();
+      }
   }
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s)
@@ -572,8 +562,8 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
   if (r.any_special) {
     __syncthreads();  // values staged, marks complete
     for (uint32_t h = tid; h < (uint32_t)kHashSlots; h += kThreads) {
-      const uint32_t off = sl.hkeys[h];
-      if (off != kEmptySlot) s_x[off] = apply_special(p.bias_ids, p.bias_values, r, s_x[off], sl.hvals[h], c0 + off);
+      const uint32_t off = s_hkeys[h];
+      if (off != kEmptySlot) s_x[off] = apply_special(p.bias_ids, p.bias_values, r, s_x[off], s_hvals[h], c0 + off);
     }
     __syncthreads();
 #pragma unroll
@@ -587,15 +577,13 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
         v[s * EPL + e + 3] = q.w;
       }
   }
-  if (p.logits_out) {  // what the reference leaves in its logits argument (temperature included)
+  if (WB) {  // what the reference leaves in its logits argument (temperature included)
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s)
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
         const uint32_t idx = c0 + s * TILE + tid * EPL + e;
-        if (idx < c1)
-          publish_u32((uint32_t*)p.logits_out + (size_t)row * p.logits_out_ld + idx,
-                      __float_as_uint(v[s * EPL + e] * inv_t));
+        if (idx < c1) p.logits_out[(size_t)row * p.logits_out_ld + idx] = v[s * EPL + e] * inv_t;
       }
   }
 
@@ -647,15 +635,15 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
     const uint64_t m = __ballot(want);
     if (want) {
       const uint32_t q = base + lanes_below(m);
-      if (q < p.cap_w) publish_u64(out + q, key);
+      if (q < p.cap_w) out[q] = key;
     }
     base += (uint32_t)__popcll(m);
   }
   const uint32_t kmax32 = cand_key(ord2f(wave_max_u32(lm)) * inv_t);  // the wavefront's largest key
   if (lane == 0) {
-    const bool bad = base > p.cap_w || (r.any_special && sl.full != 0u) || !scale_ok;
-    publish_u64(p.wave_theta + wslot, bad ? ~0ull : (((uint64_t)th_ord << 32) | kmax32));
-    publish_u32(p.wave_count + wslot, bad ? 0u : base);
+    const bool bad = base > p.cap_w || (r.any_special && *s_full != 0u) || !scale_ok;
+    p.wave_theta[wslot] = bad ? ~0ull : (((uint64_t)th_ord << 32) | kmax32);
+    p.wave_count[wslot] = bad ? 0u : base;
   }
 }
 
@@ -707,13 +695,17 @@ __device__ __forceinline__ void build_marks(const Params& p, const RowXf& r, uin
 // through the scalar cache meanwhile; then the history window ids and the
 // second half. The marks are built when the window ids arrive, which waits
 // for the first half only (vector loads complete in issue order), while the
-// second half is still in flight. `vec`: 16-byte loads (the row start is
-// 16-byte aligned and V a multiple of the group size); otherwise one load per
-// logit.
-template <int DT, int SLOTS>
-__device__ __forceinline__ void stream_block(const void* __restrict__ logits, int64_t ld, uint32_t V, bool vec,
-                                             const Params& p, uint32_t row, uint32_t chunk,
-                                             StreamLds<SLOTS * (kind_f32(DT) ? 4 : 8)>& sl) {
+// second half is still in flight.
+// The arguments before the Params copy are what the first loads need; they
+// arrive in SGPRs at wave launch (kernel-argument preloading), so those loads
+// issue without waiting for a kernel-argument fetch.
+template <int DT, int SLOTS, bool VEC, bool MASK, bool WB>
+__global__ __launch_bounds__(kThreads) void stream_kernel(const void* __restrict__ logits,
+                                                          const oxs_sampling_config* __restrict__ configs,
+                                                          const uint32_t* __restrict__ history_len,
+                                                          const uint32_t* __restrict__ history, uint32_t ld,
+                                                          uint32_t S, uint32_t rpx, uint32_t V, uint32_t kflags,
+                                                          uint32_t history_ld, const Params p) {
   constexpr int EPL = kind_f32(DT) ? 4 : 8;  // logits per 16-byte load
   constexpr int TILE = kThreads * EPL;
   constexpr int CH = SLOTS * TILE;
@@ -723,15 +715,34 @@ __device__ __forceinline__ void stream_block(const void* __restrict__ logits, in
   static_assert(CH <= kMaxChunk, "chunk too large");
   static_assert(NE <= 32, "one survivor bit per logit of a lane");
 
+  __shared__ __align__(16) float s_x[NE * kThreads];  // each thread's masked raw logits (private slots)
+  __shared__ uint32_t s_hkeys[kHashSlots];
+  __shared__ uint32_t s_hvals[kHashSlots];
+  __shared__ uint32_t s_full;
+
   const uint32_t tid = threadIdx.x;
+  // the block's (row, chunk). With rpx > 0 the hardware's round-robin
+  // placement of blocks on the 8 XCDs (block i on XCD i % 8) gives XCD x the
+  // chunks of rows [x * rpx, (x + 1) * rpx), so that a row's stream blocks and
+  // its tail block share one L2.
+  const uint32_t k = rpx ? grouped_index(blockIdx.x, rpx * S) : blockIdx.x;
+  const uint32_t row = k / S, chunk = k - row * S;  // (the grid is exactly batch x S blocks)
   const uint32_t c0 = chunk * CH;
   const uint32_t c1 = min(c0 + (uint32_t)CH, V);
+
+  // The row's record (config dwords in lanes 0-25, history length in lane
+  // 26), one vector load per lane issued before any logit: vector loads
+  // complete in issue order, so waiting for it waits for nothing else.
+  const uint32_t lane = tid & 63;
+  const uint32_t* cfgw = (const uint32_t*)(configs + ((kflags & kKShared) ? 0u : row));
+  const uint32_t rec = lane < 26u ? cfgw[lane] : (lane == 26u && (kflags & kKHistory) ? history_len[row] : 0u);
+  __builtin_amdgcn_sched_barrier(0);
 
   uint32_t raw[SLOTS][EPL];
   const char* rowp = (const char*)logits + (size_t)row * (size_t)ld * ESZ;
   auto load_slot = [&](int s) {
     const uint32_t base = c0 + s * TILE + tid * EPL;
-    if (vec) {
+    if constexpr (VEC) {
       // V is a multiple of EPL here: past-the-end groups re-read the row's
       // last group (in bounds) and their values are dropped later.
       const uint32_t at = base < c1 ? base : V - EPL;
@@ -748,7 +759,7 @@ __device__ __forceinline__ void stream_block(const void* __restrict__ logits, in
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
         const uint32_t idx = base + e;
-        raw[s][e] = __float_as_uint(load_logit<DT>(p, row, idx < c1 ? idx : V - 1));
+        raw[s][e] = __float_as_uint(load_logit<DT>(p, row, idx < c1 ? idx : p.V - 1));
       }
     }
   };
@@ -756,50 +767,57 @@ __device__ __forceinline__ void stream_block(const void* __restrict__ logits, in
 #pragma unroll
   for (int s = 0; s < H1; ++s) load_slot(s);
 #pragma unroll
-  for (int s = 0; s < SLOTS; ++s) mw[s] = 0xffffffffu;
-  if (p.mask) {
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
+  for (int s = 0; s < SLOTS; ++s) {
+    mw[s] = 0xffffffffu;
+    if constexpr (MASK) {
       const uint32_t b2 = c0 + s * TILE + tid * EPL;
-      mw[s] = p.mask[(size_t)row * p.mask_ld + ((b2 < c1 ? b2 : V - 1) >> 5)];
+      mw[s] = p.mask[(size_t)row * p.mask_ld + ((b2 < c1 ? b2 : p.V - 1) >> 5)];
     }
   }
   for (uint32_t i = tid; i < (uint32_t)kHashSlots; i += kThreads) {
-    sl.hkeys[i] = kEmptySlot;
-    sl.hvals[i] = 0;
+    s_hkeys[i] = kEmptySlot;
+    s_hvals[i] = 0;
   }
-  if (tid == 0) sl.full = 0;
+  if (tid == 0) s_full = 0;
   __builtin_amdgcn_sched_barrier(0);
-  const RowIn rin = load_row_in(p, row);
-  const RowXf r = make_row_xf_h(p, rin.cfg, rin.history_len);
+  oxs_sampling_config cfg;
+  {
+    uint32_t w[26];
+#pragma unroll
+    for (int i = 0; i < 26; ++i) w[i] = (uint32_t)__builtin_amdgcn_readlane((int)rec, i);
+    memcpy(&cfg, w, sizeof(cfg));
+  }
+  const uint32_t hlen = (uint32_t)__builtin_amdgcn_readlane((int)rec, 26);
+  if ((kflags & kKDecode) && cfg.temperature <= 1e-6f) raw_argmax_config(cfg);  // continuous_batching.rs:961
+  const RowXf r = make_row_xf(cfg, hlen, V, history_ld, kflags);
   // history window ids, read without a branch (an in-bounds dummy address
   // where the row has none)
   uint32_t hv[kHistUnroll];
-  const uint32_t* hsrc = r.use_hist ? p.history + (size_t)row * p.history_ld + r.wstart : (const uint32_t*)p.configs;
+  const uint32_t* hsrc = r.use_hist ? history + (size_t)row * history_ld + r.wstart : (const uint32_t*)configs;
   const uint32_t hn = r.use_hist ? r.wn : 0u;
 #pragma unroll
   for (int q = 0; q < kHistUnroll; ++q) {
     const uint32_t j = tid + q * kThreads;
-    hv[q] = hsrc[j < hn ? j : 0u];
+    // (a relaxed atomic load: the compiler keeps it here, ahead of the second
+    // half, instead of sinking it into the branch that reads it)
+    hv[q] = __hip_atomic_load(hsrc + (j < hn ? j : 0u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
   }
+  __builtin_amdgcn_sched_barrier(0);  // the history window ahead of the second half
 #pragma unroll
   for (int s = H1; s < SLOTS; ++s) load_slot(s);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (kind_softcap(DT)) {
-    if (vec) {  // (the one-per-logit loads above went through load_logit)
+  if constexpr (kind_softcap(DT) && VEC) {  // (the scalar loads above went through load_logit)
 #pragma unroll
-      for (int s = 0; s < SLOTS; ++s)
+    for (int s = 0; s < SLOTS; ++s)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e)
-          raw[s][e] = __float_as_uint(softcap_of(__uint_as_float(raw[s][e]), p.softcap));
-    }
+      for (int e = 0; e < EPL; ++e) raw[s][e] = __float_as_uint(softcap_of(__uint_as_float(raw[s][e]), p.softcap));
   }
   if (r.any_special) {
     __syncthreads();  // tables cleared
-    build_marks(p, r, row, c0, c1, hv, sl.hkeys, sl.hvals, &sl.full);
+    build_marks(p, r, row, c0, c1, hv, s_hkeys, s_hvals, &s_full);
   }
 
-  process_unit<DT, SLOTS>(p, row, chunk, r, raw, mw, sl);
+  process_unit<DT, SLOTS, VEC, MASK, WB>(p, row, chunk, r, raw, mw, s_x, s_hkeys, s_hvals, &s_full);
 }
 
 // ---------------------------------------------------------------- tail helpers
@@ -916,8 +934,7 @@ __device__ __forceinline__ float transformed_logit(const Params& p, const RowXf&
 }
 
 // Exact top-M of a whole row without the candidate sets: a radix select over
-// all V keys, re-reading the row once per digit, kTableMax ids at a time (the
-// penalty table covers one such piece). Used only when the candidate
+// all V keys, re-reading the row once per digit. Used only when the candidate
 // keys cannot be proven to hold the row's top M. Writes the top min(M, pool)
 // keys to out (unordered); returns that count.
 template <int DT>
@@ -932,8 +949,9 @@ __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowX
     const int shift = 56 - 8 * d;
     hist[tid] = 0;
     __syncthreads();
-    for (uint32_t c0 = 0; c0 < p.V; c0 += kTableMax) {
-      const uint32_t c1 = min(c0 + (uint32_t)kTableMax, p.V);
+    for (uint32_t c = 0; c < p.S; ++c) {
+      const uint32_t c0 = c * p.CH;
+      const uint32_t c1 = min(c0 + p.CH, p.V);
       if (r.any_special) build_table(p, r, row, c0, c1, table);
       for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
         const float y = transformed_logit<DT>(p, r, row, i, c0, table);
@@ -965,8 +983,9 @@ __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowX
   }
   if (tid == 0) ts.counter = 0;
   __syncthreads();
-  for (uint32_t c0 = 0; c0 < p.V; c0 += kTableMax) {
-    const uint32_t c1 = min(c0 + (uint32_t)kTableMax, p.V);
+  for (uint32_t c = 0; c < p.S; ++c) {
+    const uint32_t c0 = c * p.CH;
+    const uint32_t c1 = min(c0 + p.CH, p.V);
     if (r.any_special) build_table(p, r, row, c0, c1, table);
     for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
       const uint32_t k = cand_key(transformed_logit<DT>(p, r, row, i, c0, table));
@@ -1181,8 +1200,9 @@ struct RowState {
 // is one 8-byte system-scope store of (the row's step count << 32 | token),
 // written through to host memory: the host polls each slot for its expected
 // count, so no row waits for another or for the store's acknowledgement.
+template <int DT>
 __device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, uint32_t token, const RowState& rs) {
-  if (!(p.flags & kFlagDecode)) return;
+  if constexpr (!kind_decode(DT)) return;
   if (p.dec_token) p.dec_token[row] = token;
   if (p.dec_pos) p.dec_pos[row] = rs.dec_pos + 1;
   if (p.dec_count) p.dec_count[row] = rs.dec_count + 1u;
@@ -1196,13 +1216,14 @@ __device__ __forceinline__ void decode_advance(const Params& p, uint32_t row, ui
 
 // A row that ends before the chain. A raw decode row leaves the caller's
 // candidates buffer as it was.
+template <int DT>
 __device__ __forceinline__ void write_row_result(const Params& p, uint32_t row, uint32_t token, int32_t status,
                                                  const RowState& rs) {
   if (threadIdx.x == 0) {
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
     if (p.out_kept_count && !rs.raw) p.out_kept_count[row] = 0;
-    decode_advance(p, row, token, rs);
+    decode_advance<DT>(p, row, token, rs);
   }
 }
 
@@ -1271,6 +1292,7 @@ __device__ __forceinline__ uint32_t wave_compact(uint32_t* ids, float* pr, uint3
 // block barriers: parallel stages split the candidates over the lanes; the
 // reference's ordered sums run in every lane at once (seq_chain), so each lane
 // holds each result.
+template <int DT>
 __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_config& c, uint32_t row, uint32_t n,
                            ChainBufs bf, const RowState& rs, const LibmTables& tab) {
   const uint32_t l = threadIdx.x;
@@ -1488,7 +1510,7 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
     p.out_tokens[row] = token;
     if (p.out_status) p.out_status[row] = status;
     if (p.out_kept_count && !rs.raw) p.out_kept_count[row] = len;
-    decode_advance(p, row, token, rs);
+    decode_advance<DT>(p, row, token, rs);
   }
   const uint32_t nk = rs.raw ? 0u : (uint32_t)min((int64_t)len, p.kept_ld);
   for (uint32_t i = l; i < nk; i += 64) {
@@ -1507,11 +1529,11 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t k, float vmax, float scal
   return min((uint32_t)((vmax - key_value(k)) * scale), (uint32_t)kBuckets - 1);
 }
 
-// Fallback selection: all kept register keys (bit q of vm) into tmp and a
-// bitonic sort there (descending). Returns the number of kept keys.
+// Fallback selection: all kept register keys (bit q of vm) into tmp, a bitonic
+// sort, the first meff into out. Returns the number of kept keys.
 template <int PER>
 __device__ uint32_t sort_select(const uint64_t (&lk)[PER], uint32_t vm, uint32_t M, uint64_t* tmp,
-                                TailShared& ts) {
+                                uint64_t* out, TailShared& ts) {
   const uint32_t cnt = (uint32_t)__popc(vm);
   uint32_t n;
   uint32_t pos = block_excl_scan(cnt, &n, ts.scan_scratch);
@@ -1519,8 +1541,11 @@ __device__ uint32_t sort_select(const uint64_t (&lk)[PER], uint32_t vm, uint32_t
   for (int q = 0; q < PER; ++q)
     if ((vm >> q) & 1u) tmp[pos++] = lk[q];
   __syncthreads();
-  if (min(M, n) == 0) return 0;
+  const uint32_t meff = min(M, n);
+  if (meff == 0) return 0;
   bitonic_sort<false>(tmp, n);
+  for (uint32_t i = threadIdx.x; i < meff; i += kThreads) out[i] = tmp[i];
+  __syncthreads();
   return n;
 }
 
@@ -1635,41 +1660,30 @@ __device__ void keys_to_chain(const uint64_t* keys, uint32_t n, uint32_t* ids, f
   __syncthreads();
 }
 
-// LDS of the tail. `area` holds the bucket scatter, the sorted keys of the
-// sort path, the exact path's penalty table and the chain's scratch arrays;
-// `chain` holds the chain's ids and probabilities (and the exact path's
-// selected keys before they are sorted). The DRY pass uses area and chain
-// together (they are adjacent).
-constexpr int kChainScratchWords = (3 * kChainLd * 4 + kChainLd * 8) / 8;
-constexpr int tail_area_words(int per) {
-  return per * kThreads > kChainScratchWords ? per * kThreads : kChainScratchWords;
-}
-template <int PER>
-struct TailLds {
-  uint64_t area[tail_area_words(PER)];
-  uint32_t chain[2 * kChainLd];
-  float hit[16];
-  uint32_t bcount[kBuckets + 64];  // + one dummy slot per lane
-  uint32_t bstart[kWavesPerBlock][kBuckets];  // one copy per wavefront
-  TailShared ts;
-  LibmTables tab;
-};
-static_assert(tail_area_words(8) * 8 >= kTableMax * 4, "the exact path's table fits the area");
-static_assert(sizeof(uint64_t) * tail_area_words(8) + sizeof(uint32_t) * 2 * kChainLd >=
-                  sizeof(uint32_t) * (kDryMax + 3 * kDryHash),
-              "the DRY pass fits area and chain");
-static_assert(sizeof(uint32_t) * 2 * kChainLd >= sizeof(uint64_t) * kMaxM, "the exact path's keys fit chain");
-
-// The tail of one row, run by the row's last stream block: reads the row's
-// candidate keys and wavefront records (written by the row's stream blocks),
-// selects and sorts the top M, and runs the chain after the selection.
 template <int DT, int PER>
-__device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<PER>& t) {
+// Leading arguments: what the first loads need, preloaded into SGPRs as in
+// stream_kernel.
+__global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restrict__ wave_theta,
+                                                        const uint64_t* __restrict__ lists,
+                                                        const uint32_t* __restrict__ wave_count,
+                                                        const uint64_t* __restrict__ libm, uint32_t S, uint32_t cap_w,
+                                                        uint32_t cap_shift, uint32_t rpx, uint32_t B, const Params p) {
+  __shared__ __align__(16) uint64_t s_keys[kTailArea];  // bucket scatter / sort / exact-path table / chain scratch
+  static_assert(kTailArea >= PER * kThreads && kTailArea * 2 >= kMaxChunk, "tail LDS area");
+  __shared__ __align__(16) uint64_t s_top[kMaxM];       // sorted top-M keys (sort and exact paths)
+  __shared__ __align__(16) uint32_t s_ids[kChainLd];
+  __shared__ __align__(16) float s_pr[kChainLd];
+  __shared__ __align__(16) float s_hit[16];
+  __shared__ __align__(16) uint32_t s_bcount[kBuckets + 64];  // + one dummy slot per lane
+  __shared__ __align__(16) uint32_t s_bstart_all[kWavesPerBlock][kBuckets];  // one copy per wavefront
+  __shared__ TailShared ts;
+  __shared__ LibmTables s_tab;
+  static_assert(sizeof(uint32_t) * kChainLd * 3 + sizeof(uint64_t) * kChainLd <= sizeof(s_keys),
+                "chain scratch fits the key area");
+
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t S = p.S, cap_w = p.cap_w, cap_shift = p.cap_shift;
-  uint32_t* s_ids = t.chain;
-  float* s_pr = (float*)(t.chain + kChainLd);
-  TailShared& ts = t.ts;
+  const uint32_t row = rpx ? grouped_index(blockIdx.x, rpx) : blockIdx.x;
+  if (row >= B) return;
 
   // 1. the row's reads, issued before anything waits: the wavefront
   // thresholds, the candidate slots (two per 16-byte load) with the count of
@@ -1683,21 +1697,22 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
 #pragma unroll
   for (int q = 0; q < kRecPer; ++q) {
     const uint32_t w = lane + 64u * q;
-    wr[q] = collect_u64(p.wave_theta + (size_t)row * W + (w < W ? w : W - 1u));
+    wr[q] = wave_theta[(size_t)row * W + (w < W ? w : W - 1u)];
   }
   uint64_t lk[PER];
   uint32_t lc[PER / 2];
-  const uint64_t* lrow = p.lists + (size_t)row * span;
-  const uint32_t* wcrow = p.wave_count + (size_t)row * W;
+  const ulonglong2* lrow = (const ulonglong2*)(lists + (size_t)row * span);
+  const uint32_t* wcrow = wave_count + (size_t)row * W;
 #pragma unroll
   for (int q = 0; q < PER / 2; ++q) {  // unconditional loads (clamped index): no branches between them
     const uint32_t pair = tid + q * kThreads;
     const uint32_t at = 2u * pair < span ? pair : 0u;
-    lk[2 * q] = collect_u64(lrow + 2u * at);
-    lk[2 * q + 1] = collect_u64(lrow + 2u * at + 1u);
-    lc[q] = collect_u32(wcrow + ((2u * at) >> cap_shift));
+    const ulonglong2 k2 = lrow[at];
+    lk[2 * q] = k2.x;
+    lk[2 * q + 1] = k2.y;
+    lc[q] = wcrow[(2u * at) >> cap_shift];
   }
-  const LibmEntries tabv = fetch_libm_tables(p.libm);
+  const LibmEntries tabv = fetch_libm_tables(libm);
   __builtin_amdgcn_sched_barrier(0);  // every vector read above is issued before anything waits
   const RowIn rin = load_row_in(p, row);
   const oxs_sampling_config c = rin.cfg;
@@ -1711,28 +1726,29 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
   rs.dec_pos = 0;
   rs.dec_count = 0;
   rs.dec_steps = 0;
-  if (p.flags & kFlagDecode) {
+  if constexpr (kind_decode(DT)) {
     if (p.dec_pos) rs.dec_pos = p.dec_pos[row];
     if (p.dec_count) rs.dec_count = p.dec_count[row];
     if (p.host_tokens) rs.dec_steps = p.row_steps[row];
   }
-  store_libm_tables(tabv, t.tab);
-  for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) t.bcount[i] = 0;
+  store_libm_tables(tabv, s_tab);
+  for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
+
 
   const uint32_t M = max(c.top_k, 256u);
   if (M > (uint32_t)kMaxM || (r.dry && min(r.hlen, r.dry_range) > (uint32_t)kDryMax)) {
     count_path(p, kPathNone);
-    write_row_result(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // sizes this build does not run on the device
+    write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // sizes this build does not run on the device
     return;
   }
   if (c.mirostat_mode != OXS_MIROSTAT_DISABLED && !p.mu) {
     count_path(p, kPathNone);
-    write_row_result(p, row, 0u, OXS_ROW_MISSING_STATE, rs);
+    write_row_result<DT>(p, row, 0u, OXS_ROW_MISSING_STATE, rs);
     return;
   }
-  // DRY rows: their values, then the exact path (the stream phase's
+  // DRY rows: their values, then the exact path (the stream kernel's
   // candidates do not include DRY)
-  if (r.dry) dry_pass<DT>(p, r, row, (uint32_t*)t.area, t.tab, ts);
+  if (r.dry) dry_pass<DT>(p, r, row, (uint32_t*)s_keys, s_tab, ts);
 
   // 2. the largest wavefront threshold and the largest key, from the
   // wavefront records, reduced by every wavefront on its own (a record of all
@@ -1760,12 +1776,14 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
   const bool exact = th_w == 0xffffffffu || r.dry;
   const uint64_t theta_max = exact ? ~0ull : (uint64_t)th_w << 32;
   const uint64_t kmax = (uint64_t)wave_reduce32(km_l, MaxOp{}) << 32;
-  const bool all_kept = th_w == kMinValidOrd;
+  const bool all_kept = th_w == kMinValidOrd;  // (the same in every wavefront)
   uint64_t kmin = 0;
   if (all_kept) {
     const uint64_t d = wave_min_u64(kmn);
     if (lane == 0) ts.a_kmin[wave] = d;
-    __syncthreads();
+  }
+  __syncthreads();  // every bucket count zeroed before any wavefront counts, and a_kmin complete
+  if (all_kept) {
     kmin = ts.a_kmin[0];
 #pragma unroll
     for (int w = 1; w < kWavesPerBlock; ++w) kmin = ts.a_kmin[w] < kmin ? ts.a_kmin[w] : kmin;
@@ -1791,9 +1809,9 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
   const bool linear = !exact && kmax >= theta_max && range > 0.0f && range <= __FLT_MAX__ &&
                       scale <= __FLT_MAX__ && vmax <= __FLT_MAX__ && vmin >= -__FLT_MAX__;
   uint32_t meff = 0;
-  int path = exact ? kPathExact : kPathSort;
+  int path = exact ? 2 : 1;  // 0 buckets, 1 sort, 2 exact re-scan
   uint32_t bs[PER];
-  uint32_t* s_bstart = t.bstart[wave];
+  uint32_t* s_bstart = s_bstart_all[wave];
   uint32_t last = 0;
   if (linear) {
     // histogram; the returned count is the key's slot inside its bucket. Every
@@ -1803,12 +1821,12 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
     for (int q = 0; q < PER; ++q) {
       const bool on = (vm >> q) & 1u;
       const uint32_t b = on ? bucket_of(yk[q], vmax, scale) : (uint32_t)kBuckets + lane;
-      bs[q] = b | (atomicAdd(&t.bcount[b], on ? 1u : 0u) << 16);  // bucket | slot inside the bucket
+      bs[q] = b | (atomicAdd(&s_bcount[b], on ? 1u : 0u) << 16);  // bucket | slot inside the bucket
     }
     __syncthreads();
     // bucket starts, the count N and the bucket of the M-th key, computed by
     // every wavefront (lane l owns buckets 4l .. 4l+3) into its own copy
-    const uint4 c4 = *(const uint4*)&t.bcount[lane * 4];
+    const uint4 c4 = *(const uint4*)&s_bcount[lane * 4];
     const uint32_t loc = c4.x + c4.y + c4.z + c4.w;
     const uint32_t incl = wave_incl_scan(loc);
     const uint32_t N = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
@@ -1822,20 +1840,19 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
     if (st2 < meff && st2 + c4.z >= meff) mine = lane * 4 + 2;
     if (st3 < meff && st3 + c4.w >= meff) mine = lane * 4 + 3;
     last = wave_reduce32(mine, MinOp{});  // the bucket of the meff-th key
-    if (N < M && !all_kept) path = kPathExact;
-    else if (big > kBigBucket) path = kPathSort;
-    else path = kPathBuckets;
+    if (N < M && !all_kept) path = 2;
+    else if (big > kBigBucket) path = 1;
+    else path = 0;
     wave_sync();
   }
-  count_path(p, path);
+  if (path != 1) count_path(p, path);  // (the sort path counts itself: it may end in the exact path)
 
-  if (path == kPathBuckets) {
+  if (path == 0) {
     if (meff == 0) {  // every logit -inf or NaN (:267-270)
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
+      write_row_result<DT>(p, row, 0u, OXS_ROW_EMPTY, rs);
       return;
     }
-    const uint32_t span_k = s_bstart[last] + t.bcount[last];  // keys in buckets 0 .. last
-    uint64_t* s_keys = t.area;
+    const uint32_t span_k = s_bstart[last] + s_bcount[last];  // keys in buckets 0 .. last
     uint32_t start[PER];
 #pragma unroll
     for (int q = 0; q < PER; ++q) start[q] = s_bstart[min(bs[q] & 0xffffu, (uint32_t)kBuckets - 1)];
@@ -1848,44 +1865,41 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
     for (uint32_t i = tid; i < span_k; i += kThreads) {
       const uint64_t k = s_keys[i];
       const uint32_t b = bucket_of(k, vmax, scale);
-      const uint32_t lo = s_bstart[b], hi = lo + t.bcount[b];
+      const uint32_t lo = s_bstart[b], hi = lo + s_bcount[b];
       uint32_t rank = lo;
       for (uint32_t j = lo; j < hi; ++j) rank += s_keys[j] > k ? 1u : 0u;
       if (rank < meff) {
         s_ids[rank] = ~(uint32_t)k;
-        s_pr[rank] = dexpf(key_value(k) - vmax, t.tab);
+        s_pr[rank] = dexpf(key_value(k) - vmax, s_tab);
       }
     }
     __syncthreads();
-  } else if (path == kPathSort) {
-    const uint32_t N = sort_select(yk, vm, M, t.area, ts);
-    if (N < M && !all_kept) {
-      path = kPathExact;
-    } else {
+  } else if (path == 1) {
+    const uint32_t N = sort_select(yk, vm, M, s_keys, s_top, ts);
+    if (N < M && !all_kept) path = 2;
+    count_path(p, path);
+    if (path == 1) {
       meff = min(M, N);
       if (meff == 0) {
-        write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
+        write_row_result<DT>(p, row, 0u, OXS_ROW_EMPTY, rs);
         return;
       }
-      keys_to_chain(t.area, meff, s_ids, s_pr, t.tab);
+      keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
     }
   }
-  if (path == kPathExact) {
-    uint64_t* sel = (uint64_t*)t.chain;  // the selected keys, then sorted in place
-    meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)t.area, t.bcount, sel, ts);
+  if (path == 2) {
+    meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)s_keys, s_bcount, s_top, ts);
     if (meff == 0) {
-      write_row_result(p, row, 0u, OXS_ROW_EMPTY, rs);
+      write_row_result<DT>(p, row, 0u, OXS_ROW_EMPTY, rs);
       return;
     }
-    bitonic_sort<false>(sel, meff);
-    for (uint32_t i = tid; i < meff; i += kThreads) t.area[i] = sel[i];
-    __syncthreads();
-    keys_to_chain(t.area, meff, s_ids, s_pr, t.tab);
+    bitonic_sort<false>(s_top, meff);
+    keys_to_chain(s_top, meff, s_ids, s_pr, s_tab);
   }
 
   // 5. the chain after the top-M selection, in the first wavefront
   if (wave != 0) return;
-  uint32_t* scratch = (uint32_t*)t.area;
+  uint32_t* scratch = (uint32_t*)s_keys;
   ChainBufs bf;
   bf.ids = s_ids;
   bf.pr = s_pr;
@@ -1893,56 +1907,8 @@ __device__ __forceinline__ void tail_row(const Params& p, uint32_t row, TailLds<
   bf.pr_b = (float*)(scratch + kChainLd);
   bf.aux = (float*)(scratch + 2 * kChainLd);
   bf.aux64 = (uint64_t*)(scratch + 3 * kChainLd);
-  bf.hit = t.hit;
-  wave_chain(p, c, row, meff, bf, rs, t.tab);
-}
-
-// ---------------------------------------------------------------- the sampling kernel
-
-// One launch per batch; grid = rows x chunks. Every block runs the stream
-// phase over its (row, chunk). The row's blocks then count themselves on the
-// row's arrival counter, and the last one to arrive runs the row's tail. Each
-// block's candidate keys and wavefront records are in memory before its count:
-// they are stored through to memory, every thread waits for its own stores and
-// the block meets at a barrier before one thread counts; the last block reads
-// the other blocks' keys with loads that bypass its caches. The last block also
-// sets the counter back to zero for the next call. Rows complete in the order their blocks are
-// dispatched, so the tails of early rows run while later rows still stream.
-// The leading arguments are what the first loads need; they arrive in SGPRs at
-// wave launch (kernel-argument preloading), so those loads issue without
-// waiting for a kernel-argument fetch.
-template <int DT, int SLOTS, int PER>
-__global__ __launch_bounds__(kThreads) void sample_kernel(const void* __restrict__ logits, int64_t ld, uint32_t S,
-                                                          uint32_t rpx, uint32_t B, uint32_t V, uint32_t vec,
-                                                          const Params p) {
-  constexpr int NE = SLOTS * (kind_f32(DT) ? 4 : 8);
-  __shared__ __align__(16) union {
-    StreamLds<NE> s;
-    TailLds<PER> t;
-  } lds;
-  __shared__ uint32_t s_last;
-
-  // the block's (row, chunk). With rpx > 0 the hardware's round-robin
-  // placement of blocks on the 8 XCDs (block i on XCD i % 8) gives XCD x the
-  // chunks of rows [x * rpx, (x + 1) * rpx), so that a row's blocks share one
-  // L2.
-  const uint32_t k = rpx ? grouped_index(blockIdx.x, rpx * S) : blockIdx.x;
-  const uint32_t row = k / S, chunk = k - row * S;
-  if (row >= B) return;
-  stream_block<DT, SLOTS>(logits, ld, V, vec != 0u, p, row, chunk, lds.s);
-
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's keys and records have reached memory
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* ctr = p.tickets + (size_t)row * kTicketStride;
-    const uint32_t n = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    const uint32_t is_last = n + 1u == S ? 1u : 0u;
-    if (is_last) publish_u32(ctr, 0u);
-    s_last = is_last;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  tail_row<DT, PER>(p, row, lds.t);
+  bf.hit = s_hit;
+  wave_chain<DT>(p, c, row, meff, bf, rs, s_tab);
 }
 
 // ---------------------------------------------------------------- argmax
@@ -2044,38 +2010,68 @@ static bool choose_geometry(uint32_t B, uint32_t V, int dtype, Geometry* g) {
   return true;
 }
 
-// PER: candidate key slots per tail thread, 2048 keys per row (8) or 4096
-// past 64 wavefront records (16).
-template <int DT, int SLOTS>
-static hipError_t launch_per(const Params& p, uint32_t grid, bool vec, hipStream_t st) {
-  if ((uint64_t)p.S * kWavesPerBlock * p.cap_w > (uint64_t)kUnionMax)
-    hipLaunchKernelGGL((sample_kernel<DT, SLOTS, kUnionBig / kThreads>), dim3(grid), dim3(kThreads), 0, st, p.logits,
-                       p.ld, p.S, p.rpx, p.B, p.V, vec ? 1u : 0u, p);
+template <int DT, int SLOTS, bool VEC, bool MASK>
+static hipError_t launch_stream(const Params& p, uint32_t grid, hipStream_t st) {
+  const uint32_t* hl = (const uint32_t*)p.history_len;
+  const uint32_t* h = (const uint32_t*)p.history;
+  const uint32_t hld = (uint32_t)p.history_ld, ld = (uint32_t)p.ld;
+  const uint32_t kflags = ((p.flags & OXS_FLAG_SHARED_CONFIG) ? kKShared : 0u) |
+                          ((p.flags & kFlagDecode) ? kKDecode : 0u) | ((h && hl) ? kKHistory : 0u) |
+                          (p.bias_ids ? kKBias : 0u) | (p.ban_ids ? kKBan : 0u);
+  if (p.logits_out)
+    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, true>), dim3(grid), dim3(kThreads), 0, st, p.logits,
+                       p.configs, hl, h, ld, p.S, p.rpx, p.V, kflags, hld, p);
   else
-    hipLaunchKernelGGL((sample_kernel<DT, SLOTS, kPer>), dim3(grid), dim3(kThreads), 0, st, p.logits, p.ld, p.S,
-                       p.rpx, p.B, p.V, vec ? 1u : 0u, p);
+    hipLaunchKernelGGL((stream_kernel<DT, SLOTS, VEC, MASK, false>), dim3(grid), dim3(kThreads), 0, st, p.logits,
+                       p.configs, hl, h, ld, p.S, p.rpx, p.V, kflags, hld, p);
   return hipGetLastError();
 }
 
-template <int DT>
-static hipError_t launch_slots(int slots, const Params& p, uint32_t grid, bool vec, hipStream_t st) {
+template <int DT, bool VEC, bool MASK>
+static hipError_t launch_slots(int slots, const Params& p, uint32_t grid, hipStream_t st) {
   switch (slots) {
     case 8:
-      if constexpr (kind_f32(DT)) return launch_per<DT, 8>(p, grid, vec, st);
+      if constexpr (kind_f32(DT)) return launch_stream<DT, 8, VEC, MASK>(p, grid, st);
       return hipErrorInvalidValue;  // bf16 chunks stop at 4 slots (8192 logits)
-    case 4: return launch_per<DT, 4>(p, grid, vec, st);
-    case 2: return launch_per<DT, 2>(p, grid, vec, st);
-    default: return launch_per<DT, 1>(p, grid, vec, st);
+    case 4: return launch_stream<DT, 4, VEC, MASK>(p, grid, st);
+    case 2: return launch_stream<DT, 2, VEC, MASK>(p, grid, st);
+    default: return launch_stream<DT, 1, VEC, MASK>(p, grid, st);
   }
 }
 
-static hipError_t launch_kind(int kind, int slots, const Params& p, uint32_t grid, bool vec, hipStream_t st) {
-  constexpr int F = OXS_DTYPE_F32, H = OXS_DTYPE_BF16, S = kKindSoftcap;
+// KIND: the tail's kind; the stream kernel's is the same without the decode bit.
+template <int KIND>
+static hipError_t launch_all(int slots, bool vec, bool mask, const Params& p, uint32_t grid_a,
+                             uint32_t grid_b, hipStream_t st) {
+  constexpr int SK = KIND & ~kKindDecode;
+  hipError_t e;
+  if (vec) e = mask ? launch_slots<SK, true, true>(slots, p, grid_a, st) : launch_slots<SK, true, false>(slots, p, grid_a, st);
+  else e = mask ? launch_slots<SK, false, true>(slots, p, grid_a, st) : launch_slots<SK, false, false>(slots, p, grid_a, st);
+  if (e != hipSuccess) return e;
+  // the row's candidate union: 2048 keys, or 4096 past 64 wavefront records
+  if ((uint64_t)p.S * kWavesPerBlock * p.cap_w > (uint64_t)kUnionMax)
+    hipLaunchKernelGGL((tail_kernel<KIND, kUnionBig / kThreads>), dim3(grid_b), dim3(kThreads), 0, st,
+                       (const uint64_t*)p.wave_theta, (const uint64_t*)p.lists, (const uint32_t*)p.wave_count, p.libm,
+                       p.S, p.cap_w, p.cap_shift, p.rpx, p.B, p);
+  else
+    hipLaunchKernelGGL((tail_kernel<KIND, kPer>), dim3(grid_b), dim3(kThreads), 0, st, (const uint64_t*)p.wave_theta,
+                       (const uint64_t*)p.lists, (const uint32_t*)p.wave_count, p.libm, p.S, p.cap_w, p.cap_shift,
+                       p.rpx, p.B, p);
+  return hipGetLastError();
+}
+
+static hipError_t launch_kind(int kind, int slots, bool vec, bool mask, const Params& p, uint32_t grid_a,
+                              uint32_t grid_b, hipStream_t st) {
+  constexpr int F = OXS_DTYPE_F32, H = OXS_DTYPE_BF16, S = kKindSoftcap, D = kKindDecode;
   switch (kind) {
-    case F: return launch_slots<F>(slots, p, grid, vec, st);
-    case H: return launch_slots<H>(slots, p, grid, vec, st);
-    case F | S: return launch_slots<F | S>(slots, p, grid, vec, st);
-    case H | S: return launch_slots<H | S>(slots, p, grid, vec, st);
+    case F: return launch_all<F>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H: return launch_all<H>(slots, vec, mask, p, grid_a, grid_b, st);
+    case F | S: return launch_all<F | S>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H | S: return launch_all<H | S>(slots, vec, mask, p, grid_a, grid_b, st);
+    case F | D: return launch_all<F | D>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H | D: return launch_all<H | D>(slots, vec, mask, p, grid_a, grid_b, st);
+    case F | S | D: return launch_all<F | S | D>(slots, vec, mask, p, grid_a, grid_b, st);
+    case H | S | D: return launch_all<H | S | D>(slots, vec, mask, p, grid_a, grid_b, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -2094,7 +2090,6 @@ struct oxs_sampler {
   uint64_t* dry_list;
   uint32_t* dry_count;
   uint32_t* row_steps;  // [max_batch] decode steps each row has handed to the host
-  uint32_t* tickets;    // [max_batch][kTicketStride] per-row arrival counters, zero between calls
   uint32_t* path_counts;  // [kPathKinds] rows per top-M selection path
   bool count_paths;
   size_t bytes;
@@ -2183,13 +2178,10 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
                   hipMalloc((void**)&s->dry_count, B * sizeof(uint32_t)) == hipSuccess &&
                   hipMalloc((void**)&s->row_steps, B * sizeof(uint32_t)) == hipSuccess &&
                   hipMemset(s->row_steps, 0, B * sizeof(uint32_t)) == hipSuccess &&
-                  hipMalloc((void**)&s->tickets, B * oxs::kTicketStride * sizeof(uint32_t)) == hipSuccess &&
-                  hipMemset(s->tickets, 0, B * oxs::kTicketStride * sizeof(uint32_t)) == hipSuccess &&
                   hipMalloc((void**)&s->path_counts, oxs::kPathKinds * sizeof(uint32_t)) == hipSuccess &&
                   hipMemset(s->path_counts, 0, oxs::kPathKinds * sizeof(uint32_t)) == hipSuccess;
   s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t) +
-             B * (oxs::kDryMax * sizeof(uint64_t) + (2 + oxs::kTicketStride) * sizeof(uint32_t)) +
-             oxs::kPathKinds * sizeof(uint32_t);
+             B * (oxs::kDryMax * sizeof(uint64_t) + 2 * sizeof(uint32_t)) + oxs::kPathKinds * sizeof(uint32_t);
   if (ok) {  // the libm tables, as bit patterns, in the workspace
     uint64_t host[oxs::kLibmWords];
     ok = hipMemcpyFromSymbol(host, HIP_SYMBOL(oxs_libm::kExp2Tab), 32 * sizeof(uint64_t)) == hipSuccess &&
@@ -2215,7 +2207,6 @@ int oxs_sampler_destroy(oxs_sampler* s) {
   if (s->dry_list) (void)hipFree(s->dry_list);
   if (s->dry_count) (void)hipFree(s->dry_count);
   if (s->row_steps) (void)hipFree(s->row_steps);
-  if (s->tickets) (void)hipFree(s->tickets);
   if (s->path_counts) (void)hipFree(s->path_counts);
   free(s);
   return OXS_OK;
@@ -2254,11 +2245,12 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
   if (b->batch > s->limits.max_batch || b->vocab > s->limits.max_vocab) return OXS_ERR_LIMITS;
   if (!b->logits || !b->configs || !b->out_tokens) return OXS_ERR_INVALID_ARGUMENT;
   if (b->logits_dtype != OXS_DTYPE_F32 && b->logits_dtype != OXS_DTYPE_BF16) return OXS_ERR_INVALID_ARGUMENT;
-  if (b->logits_ld < (int64_t)b->vocab) return OXS_ERR_INVALID_ARGUMENT;
+  if (b->logits_ld < (int64_t)b->vocab || b->logits_ld > (int64_t)UINT32_MAX) return OXS_ERR_INVALID_ARGUMENT;
   if (b->allowed_mask && b->mask_ld != 0 && b->mask_ld < (int64_t)((b->vocab + 31) / 32))
     return OXS_ERR_INVALID_ARGUMENT;  // 0: one mask for every row
   if (!b->uniforms && !b->rng_state) return OXS_ERR_INVALID_ARGUMENT;
-  if (b->history && (!b->history_len || b->history_ld <= 0)) return OXS_ERR_INVALID_ARGUMENT;
+  if (b->history && (!b->history_len || b->history_ld <= 0 || b->history_ld > (int64_t)UINT32_MAX))
+    return OXS_ERR_INVALID_ARGUMENT;
   if (b->flags & OXS_FLAG_RECORD_HISTORY) {
     if (!b->history || !b->history_len || (int64_t)b->history_cap > b->history_ld) return OXS_ERR_INVALID_ARGUMENT;
   }
@@ -2316,6 +2308,7 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
   p.libm = s->libm;
   p.dry_list = s->dry_list;
   p.dry_count = s->dry_count;
+  p.path_counts = s->count_paths ? s->path_counts : nullptr;
   if (io) {
     p.flags |= kFlagDecode;
     p.dec_token = io->current_token;
@@ -2324,16 +2317,17 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
     p.host_tokens = io->host_tokens;
     p.row_steps = s->row_steps;
   }
-  p.tickets = s->tickets;
-  p.path_counts = s->count_paths ? s->path_counts : nullptr;
   // Group rows by XCD when the batch divides evenly over the 8 XCDs.
   p.rpx = (b->batch % 8 == 0) ? b->batch / 8 : 0;
   const uint32_t epl = b->logits_dtype == OXS_DTYPE_F32 ? 4 : 8;
   const bool vec = ((uintptr_t)b->logits % 16 == 0) && ((size_t)b->logits_ld % epl == 0) &&
                    (b->vocab % epl == 0);
+  const bool mask = b->allowed_mask != nullptr;
+  const uint32_t grid_a = b->batch * g.S;
+  const uint32_t grid_b = b->batch;
   hipStream_t st = (hipStream_t)stream;
-  const int kind = b->logits_dtype | (p.softcap > 0.0f ? kKindSoftcap : 0);
-  const hipError_t e = launch_kind(kind, g.slots, p, b->batch * g.S, vec, st);
+  const int kind = b->logits_dtype | (p.softcap > 0.0f ? kKindSoftcap : 0) | (io ? kKindDecode : 0);
+  const hipError_t e = launch_kind(kind, g.slots, vec, mask, p, grid_a, grid_b, st);
   return e == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }
 
