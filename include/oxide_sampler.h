@@ -241,6 +241,28 @@ int oxs_sampler_path_counts(const oxs_sampler* sampler, uint32_t counts[4]);
 int oxs_sample_batch(oxs_sampler* sampler, const oxs_batch* batch, void* stream);
 
 /*
+ * oxs_sample_batch without a sampler and without any allocation: the same
+ * kernels and results, with the workspace in a fixed device array of this
+ * library (one per GPU, about 11 MiB, held until the process ends) instead
+ * of a sampler's. It has no counterpart in the reference; it is for callers
+ * that cannot allocate device memory: code under HIP graph capture, serving
+ * loops and harnesses that forbid hipMalloc.
+ *   - batches up to OXS_STATIC_MAX_BATCH rows of up to OXS_STATIC_MAX_VOCAB
+ *     logits; larger: OXS_ERR_LIMITS;
+ *   - runs on the calling thread's current device; the first call on a device
+ *     sets the array up (finds its address and fills its constant tables,
+ *     waiting for that on `stream`), so it must not be under stream capture
+ *     (OXS_ERR_INVALID_ARGUMENT there); later calls only launch;
+ *   - every call on one device shares that device's array: calls that overlap
+ *     on one GPU (other streams, other threads) race and give wrong results;
+ *   - per-path counting (oxs_sampler_count_paths) does not apply.
+ * Other errors as oxs_sample_batch.
+ */
+#define OXS_STATIC_MAX_BATCH 256u
+#define OXS_STATIC_MAX_VOCAB 524288u
+int oxs_sample_batch_static(const oxs_batch* batch, void* stream);
+
+/*
  * Decode-loop state beside the sampler state (ActiveSequence,
  * crates/oxide-engine/src/continuous_batching.rs:453-470), device arrays
  * unless noted; every pointer is optional.

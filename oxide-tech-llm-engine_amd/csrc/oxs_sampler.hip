@@ -31,6 +31,8 @@
 // waits on the host; all workspace comes from the sampler handle.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <mutex>
 #include <stdlib.h>
 #include <string.h>
 
@@ -2095,6 +2097,96 @@ struct oxs_sampler {
   size_t bytes;
 };
 
+namespace oxs {
+
+// The device memory one sampling call uses besides its inputs and outputs,
+// and the batch it is sized for: a sampler's allocations, or the static
+// array of the no-allocation entry point.
+struct Workspace {
+  uint32_t max_batch, max_vocab;
+  uint64_t* lists;        // [max_batch][union slots]
+  uint64_t* wave_theta;   // [max_batch][kMaxChunks * kWavesPerBlock]
+  uint32_t* wave_count;   // [max_batch][kMaxChunks * kWavesPerBlock]
+  uint64_t* libm;         // [kLibmWords]
+  uint64_t* dry_list;     // [max_batch][kDryMax]
+  uint32_t* dry_count;    // [max_batch]
+  uint32_t* row_steps;    // [max_batch] (decode steps only; may be null otherwise)
+  uint32_t* path_counts;  // [kPathKinds] or null (counting off)
+};
+
+__device__ __forceinline__ uint64_t libm_word(uint32_t i) {  // the workspace's libm layout
+  if (i < 32u) return oxs_libm::kExp2Tab[i];
+  if (i < 48u) return (uint64_t)__double_as_longlong(oxs_libm::kLogInvc[i - 32u]);
+  if (i < 64u) return (uint64_t)__double_as_longlong(oxs_libm::kLnLogc[i - 48u]);
+  return (uint64_t)__double_as_longlong(oxs_libm::kLog2Logc[i - 64u]);
+}
+
+// Copies the libm tables into a workspace (one block; threads past
+// kLibmWords do nothing).
+__global__ void libm_fill_kernel(uint64_t* __restrict__ dst) {
+  if (threadIdx.x < (uint32_t)kLibmWords) dst[threadIdx.x] = libm_word(threadIdx.x);
+}
+
+// ------------------------------------------------ no-allocation workspace
+// The workspace of oxs_sample_batch_static: one file-scope device array per
+// GPU, laid out as below for OXS_STATIC_MAX_BATCH rows of up to
+// OXS_STATIC_MAX_VOCAB logits. Host code never uses `scratch` itself (on the
+// host the name stands for no device address): each device's address comes
+// from hipGetSymbolAddress, once, and is kept in g_static_ws.
+constexpr size_t kStaticB = OXS_STATIC_MAX_BATCH;
+constexpr size_t kStaticW = (size_t)kMaxChunks * kWavesPerBlock;  // wavefront records per row
+constexpr size_t kStOffLists = 0;                                         // u64 [B][kUnionBig]
+constexpr size_t kStOffTheta = kStOffLists + kStaticB * kUnionBig;        // u64 [B][W]
+constexpr size_t kStOffDry = kStOffTheta + kStaticB * kStaticW;           // u64 [B][kDryMax]
+constexpr size_t kStOffLibm = kStOffDry + kStaticB * kDryMax;             // u64 [kLibmWords]
+constexpr size_t kStOffCount = kStOffLibm + (size_t)kLibmWords;           // u32 [B][W]
+constexpr size_t kStOffDryCount = kStOffCount + kStaticB * kStaticW / 2;  // u32 [B]
+constexpr size_t kStaticWords = kStOffDryCount + kStaticB / 2;
+static_assert(OXS_STATIC_MAX_VOCAB <= (uint64_t)kMaxChunks * kMaxChunk, "static vocabulary beyond the row limit");
+static_assert(kStaticB % 2 == 0 && kStaticW % 2 == 0, "u32 regions start on 8-byte boundaries");
+
+static __device__ __align__(256) uint64_t scratch[kStaticWords];
+
+constexpr int kStaticMaxDevices = 64;
+struct StaticWs {
+  uint64_t* base;  // this device's copy of `scratch` (device address), null until set up
+};
+static StaticWs g_static_ws[kStaticMaxDevices];
+static std::mutex g_static_mu;
+
+// The workspace view of a device's static array.
+static Workspace static_workspace(uint64_t* base) {
+  Workspace w;
+  w.max_batch = OXS_STATIC_MAX_BATCH;
+  w.max_vocab = OXS_STATIC_MAX_VOCAB;
+  w.lists = base + kStOffLists;
+  w.wave_theta = base + kStOffTheta;
+  w.wave_count = (uint32_t*)(base + kStOffCount);
+  w.libm = base + kStOffLibm;
+  w.dry_list = base + kStOffDry;
+  w.dry_count = (uint32_t*)(base + kStOffDryCount);
+  w.row_steps = nullptr;
+  w.path_counts = nullptr;
+  return w;
+}
+
+}  // namespace oxs
+
+static oxs::Workspace sampler_workspace(const oxs_sampler* s) {
+  oxs::Workspace w;
+  w.max_batch = s->limits.max_batch;
+  w.max_vocab = s->limits.max_vocab;
+  w.lists = s->lists;
+  w.wave_theta = s->wave_theta;
+  w.wave_count = s->wave_count;
+  w.libm = s->libm;
+  w.dry_list = s->dry_list;
+  w.dry_count = s->dry_count;
+  w.row_steps = s->row_steps;
+  w.path_counts = s->count_paths ? s->path_counts : nullptr;
+  return w;
+}
+
 extern "C" {
 
 uint32_t oxs_abi_version(void) { return OXS_ABI_VERSION; }
@@ -2236,13 +2328,13 @@ int oxs_sampler_path_counts(const oxs_sampler* s, uint32_t* counts) {
 
 }  // extern "C"
 
-// One sampling launch pair; `io` (a decode step) may be NULL.
-static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* io, void* stream) {
+// One sampling launch pair over workspace `ws`; `io` (a decode step) may be NULL.
+static int sample_impl(const oxs::Workspace& ws, const oxs_batch* b, const oxs_decode_io* io, void* stream) {
   using namespace oxs;
-  if (!s || !b) return OXS_ERR_INVALID_ARGUMENT;
+  if (!b) return OXS_ERR_INVALID_ARGUMENT;
   if (b->vocab == 0) return OXS_ERR_SHAPE_MISMATCH;  // sampler.rs:179-181
   if (b->batch == 0) return OXS_OK;
-  if (b->batch > s->limits.max_batch || b->vocab > s->limits.max_vocab) return OXS_ERR_LIMITS;
+  if (b->batch > ws.max_batch || b->vocab > ws.max_vocab) return OXS_ERR_LIMITS;
   if (!b->logits || !b->configs || !b->out_tokens) return OXS_ERR_INVALID_ARGUMENT;
   if (b->logits_dtype != OXS_DTYPE_F32 && b->logits_dtype != OXS_DTYPE_BF16) return OXS_ERR_INVALID_ARGUMENT;
   if (b->logits_ld < (int64_t)b->vocab || b->logits_ld > (int64_t)UINT32_MAX) return OXS_ERR_INVALID_ARGUMENT;
@@ -2302,20 +2394,21 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
   p.cap_w = g.cap_w;
   p.cap_shift = (uint32_t)__builtin_ctz(g.cap_w);
   p.c_w = g.c_w;
-  p.lists = s->lists;
-  p.wave_theta = s->wave_theta;
-  p.wave_count = s->wave_count;
-  p.libm = s->libm;
-  p.dry_list = s->dry_list;
-  p.dry_count = s->dry_count;
-  p.path_counts = s->count_paths ? s->path_counts : nullptr;
+  p.lists = ws.lists;
+  p.wave_theta = ws.wave_theta;
+  p.wave_count = ws.wave_count;
+  p.libm = ws.libm;
+  p.dry_list = ws.dry_list;
+  p.dry_count = ws.dry_count;
+  p.path_counts = ws.path_counts;
   if (io) {
+    if (!ws.row_steps) return OXS_ERR_INVALID_ARGUMENT;
     p.flags |= kFlagDecode;
     p.dec_token = io->current_token;
     p.dec_pos = io->current_position;
     p.dec_count = io->generated_count;
     p.host_tokens = io->host_tokens;
-    p.row_steps = s->row_steps;
+    p.row_steps = ws.row_steps;
   }
   // Group rows by XCD when the batch divides evenly over the 8 XCDs.
   p.rpx = (b->batch % 8 == 0) ? b->batch / 8 : 0;
@@ -2334,13 +2427,40 @@ static int sample_impl(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* 
 extern "C" {
 
 int oxs_sample_batch(oxs_sampler* s, const oxs_batch* b, void* stream) {
-  if (b && (b->flags & oxs::kFlagDecode)) return OXS_ERR_INVALID_ARGUMENT;  // not a public flag
-  return sample_impl(s, b, nullptr, stream);
+  if (!s || (b && (b->flags & oxs::kFlagDecode))) return OXS_ERR_INVALID_ARGUMENT;  // not a public flag
+  return sample_impl(sampler_workspace(s), b, nullptr, stream);
 }
 
 int oxs_decode_step(oxs_sampler* s, const oxs_batch* b, const oxs_decode_io* io, void* stream) {
-  if (!io || (b && (b->flags & oxs::kFlagDecode))) return OXS_ERR_INVALID_ARGUMENT;
-  return sample_impl(s, b, io, stream);
+  if (!s || !io || (b && (b->flags & oxs::kFlagDecode))) return OXS_ERR_INVALID_ARGUMENT;
+  return sample_impl(sampler_workspace(s), b, io, stream);
+}
+
+int oxs_sample_batch_static(const oxs_batch* b, void* stream) {
+  using namespace oxs;
+  if (!b || (b->flags & kFlagDecode)) return OXS_ERR_INVALID_ARGUMENT;
+  if (b->batch > OXS_STATIC_MAX_BATCH || b->vocab > OXS_STATIC_MAX_VOCAB) return OXS_ERR_LIMITS;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return OXS_ERR_NO_DEVICE;
+  if (dev < 0 || dev >= kStaticMaxDevices) return OXS_ERR_UNSUPPORTED;
+  uint64_t* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    base = g_static_ws[dev].base;
+    if (!base) {  // this device's first call: find its copy of the array, fill the libm tables
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) return OXS_ERR_HIP;
+      if (cs != hipStreamCaptureStatusNone) return OXS_ERR_INVALID_ARGUMENT;  // set-up waits: not under capture
+      uint64_t* ptr = nullptr;
+      if (hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return OXS_ERR_HIP;
+      hipLaunchKernelGGL(libm_fill_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, ptr + kStOffLibm);
+      if (hipGetLastError() != hipSuccess || hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+        return OXS_ERR_HIP;
+      g_static_ws[dev].base = ptr;
+      base = ptr;
+    }
+  }
+  return sample_impl(static_workspace(base), b, nullptr, stream);
 }
 
 int oxs_host_alloc(size_t bytes, void** out) {

@@ -44,6 +44,9 @@ OXS_PATH_SORT = 1
 OXS_PATH_EXACT = 2
 OXS_PATH_NONE = 3
 
+OXS_STATIC_MAX_BATCH = 256
+OXS_STATIC_MAX_VOCAB = 524288
+
 # Exported symbols declared in include/oxide_sampler.h.
 EXPORTED_SYMBOLS = (
     "oxs_abi_version",
@@ -57,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "oxs_sampler_count_paths",
     "oxs_sampler_path_counts",
     "oxs_sample_batch",
+    "oxs_sample_batch_static",
     "oxs_decode_step",
     "oxs_argmax",
     "oxs_host_alloc",
@@ -222,6 +226,8 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_sampler_path_counts.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]
     lib.oxs_sample_batch.restype = ctypes.c_int
     lib.oxs_sample_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.c_void_p]
+    lib.oxs_sample_batch_static.restype = ctypes.c_int
+    lib.oxs_sample_batch_static.argtypes = [ctypes.POINTER(OxsBatch), ctypes.c_void_p]
     lib.oxs_decode_step.restype = ctypes.c_int
     lib.oxs_decode_step.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.POINTER(OxsDecodeIo),
                                     ctypes.c_void_p]

@@ -202,11 +202,18 @@ class BatchSampler:
         check(self.lib.oxs_sampler_path_counts(self.handle, c), "oxs_sampler_path_counts")
         return {"buckets": int(c[0]), "sort": int(c[1]), "exact": int(c[2]), "none": int(c[3])}
 
-    def launch(self, batch: OxsBatch, stream=None, decode: Optional[OxsDecodeIo] = None) -> None:
+    def launch(self, batch: OxsBatch, stream=None, decode: Optional[OxsDecodeIo] = None,
+               no_alloc: bool = False) -> None:
         """Raw launch of a prepared descriptor on `stream` (torch stream or None);
-        with `decode`, a decode step (oxs_decode_step)."""
+        with `decode`, a decode step (oxs_decode_step); with `no_alloc`, through
+        oxs_sample_batch_static (the library's fixed workspace, not this sampler's)."""
         s = stream if stream is not None else self.torch.cuda.current_stream(self.device)
-        if decode is None:
+        if no_alloc:
+            if decode is not None:
+                raise ValueError("oxs_sample_batch_static has no decode-step form")
+            check(self.lib.oxs_sample_batch_static(ctypes.byref(batch), ctypes.c_void_p(s.cuda_stream)),
+                  "oxs_sample_batch_static")
+        elif decode is None:
             check(self.lib.oxs_sample_batch(self.handle, ctypes.byref(batch), ctypes.c_void_p(s.cuda_stream)),
                   "oxs_sample_batch")
         else:
@@ -217,7 +224,7 @@ class BatchSampler:
                mask=None, history=None, history_len=None, history_cap: Optional[int] = None,
                record: bool = False, uniforms=None, rng_state=None, mirostat_mu=None,
                kept_ld: int = 0, logits_out=None, stream=None, decode: Optional[OxsDecodeIo] = None,
-               out: Optional[dict] = None, softcap: float = 0.0):
+               out: Optional[dict] = None, softcap: float = 0.0, no_alloc: bool = False):
         """Samples every row of `logits` ([B, V] f32/bf16 CUDA tensor).
 
         `configs` is a uint8 CUDA tensor holding B (or 1 with shared_config)
@@ -225,7 +232,8 @@ class BatchSampler:
         (tokens, status, kept_count and, with kept_ld > 0, kept_ids/kept_probs),
         the ones of `out` when given. With `decode` (an OxsDecodeIo) the call
         is a decode step (oxs_decode_step). `softcap` > 0 applies the model's
-        final logit softcap as the logits are read.
+        final logit softcap as the logits are read. `no_alloc` runs the call
+        through oxs_sample_batch_static.
         """
         t = self.torch
         dev = logits.device
@@ -280,7 +288,7 @@ class BatchSampler:
             b.logits_out = logits_out.data_ptr()
             b.logits_out_ld = int(logits_out.stride(0))
         b.logit_softcap = float(softcap)
-        self.launch(b, stream, decode)
+        self.launch(b, stream, decode, no_alloc)
         return out
 
 

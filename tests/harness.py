@@ -74,7 +74,7 @@ def to_device(w: Workload, torch):
 
 def run_gpu(w: Workload, torch, kept_ld: int = 256, record: bool = True, use_rng: bool = False,
             rng_state: Optional[np.ndarray] = None, logits_out: bool = False, logits_dev=None,
-            max_top_k: int = 256, shared_mask: bool = False) -> Result:
+            max_top_k: int = 256, shared_mask: bool = False, no_alloc: bool = False) -> Result:
     d = torch.device("cuda")
     cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
     s = gpu_sampler(w.batch, w.vocab, max_top_k)
@@ -94,7 +94,8 @@ def run_gpu(w: Workload, torch, kept_ld: int = 256, record: bool = True, use_rng
         ban_ids=torch.from_numpy(ban_ids.view(np.int32)).to(d) if ban_ids.size else None,
         mask=mask, history=hist, history_len=hlen, history_cap=w.history.shape[1], record=record,
         uniforms=None if use_rng else torch.from_numpy(w.uniforms).to(d), rng_state=rng,
-        mirostat_mu=mu, kept_ld=kept_ld, logits_out=lo, softcap=float(w.extra.get("softcap", 0.0)))
+        mirostat_mu=mu, kept_ld=kept_ld, logits_out=lo, softcap=float(w.extra.get("softcap", 0.0)),
+        no_alloc=no_alloc)
     torch.cuda.synchronize()
     return Result(
         out["tokens"].cpu().numpy().view(np.uint32), out["status"].cpu().numpy(),
