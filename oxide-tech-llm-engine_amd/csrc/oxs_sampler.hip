@@ -1288,6 +1288,50 @@ __device__ __forceinline__ uint32_t wave_compact(uint32_t* ids, float* pr, uint3
   return kept;
 }
 
+// Number of leading entries of d[lo .. lo + n) for which `holds` is false,
+// when it is false up to some point and true after it (binary lifting with
+// steps top, top / 2, ..., 1; top is the largest power of two not above n).
+template <typename P>
+__device__ __forceinline__ uint32_t count_false(const uint32_t* d, uint32_t lo, uint32_t n, uint32_t top, P holds) {
+  uint32_t cnt = 0;
+  for (uint32_t step = top; step; step >>= 1) {
+    const uint32_t at = cnt + step;
+    if (at <= n && !holds(d[lo + at - 1])) cnt = at;
+  }
+  return cnt;
+}
+
+// Typical's stable sort (sampler.rs:508) when its scores are V-shaped:
+// d (ordered score bits) non-increasing on [0, m) and non-decreasing on
+// [m, len), as |surprisal - H| is over candidates sorted by probability. The
+// rank of key (d[i] << 32 | i) then needs no comparison with every other key:
+//   i >= m: the keys of [m, i) and those of [0, m) with d <= d[i] are below it;
+//   i <  m: those of [0, m) with d < d[i], those of [first with d == d[i], i)
+//           and those of [m, len) with d < d[i],
+// each a count over one monotone run. Writes the sorted (ids, pr) to
+// (ids_b, pr_b). One wavefront.
+__device__ __forceinline__ void typical_rank_v(const uint32_t* ids, const float* pr, const uint32_t* d, uint32_t len,
+                                               uint32_t m, uint32_t* ids_b, float* pr_b) {
+  const uint32_t l = threadIdx.x & 63;
+  const uint32_t nl = m, nr = len - m;
+  const uint32_t tl = nl > 1 ? 1u << (31 - __builtin_clz(nl)) : nl;
+  const uint32_t tr = nr > 1 ? 1u << (31 - __builtin_clz(nr)) : nr;
+  for (uint32_t i = l; i < len; i += 64) {
+    const uint32_t v = d[i];
+    const uint32_t le = count_false(d, 0, nl, tl, [=](uint32_t x) { return x <= v; });  // [0, le): d > v
+    uint32_t rank;
+    if (i >= m) {
+      rank = (i - m) + (nl - le);
+    } else {
+      const uint32_t lt = count_false(d, 0, nl, tl, [=](uint32_t x) { return x < v; });  // [0, lt): d >= v
+      const uint32_t rlt = count_false(d, m, nr, tr, [=](uint32_t x) { return x >= v; });  // [m, m + rlt): d < v
+      rank = (nl - lt) + (i - le) + rlt;
+    }
+    ids_b[rank] = ids[i];
+    pr_b[rank] = pr[i];
+  }
+}
+
 // The chain after the top-M selection (sampler.rs:286-389) on the n
 // candidates in bf.ids, sorted, with bf.pr = exp(logit - max logit) (the
 // softmax numerators, :286-290), run by one wavefront (threads 0..63) with no
@@ -1430,37 +1474,60 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
     // by rank counting over (score, position) keys.
     if (c.typical_p < 1.0f && len > 1) {
       float* terms = bf.aux;
-      uint64_t* sk = bf.aux64;
-      for (uint32_t i = l; i < len; i += 64) terms[i] = pr[i] > 0.0f ? (-pr[i]) * dlogf(pr[i], tab) : 0.0f;
+      float* lg = (float*)bf.ids_b;  // ln p, until the sorted ids are written there
+      for (uint32_t i = l; i < len; i += 64) {
+        const float x = pr[i] > 0.0f ? dlogf(pr[i], tab) : 0.0f;
+        lg[i] = x;
+        terms[i] = pr[i] > 0.0f ? (-pr[i]) * x : 0.0f;
+      }
       wave_sync();
       const float entropy = seq_chain<false>(terms, len, -0.0f, 0.0f, Ident{}, bf.hit).sum;
-      for (uint32_t i = l; i < len; i += 64) {
-        const float surprisal = pr[i] > 0.0f ? -dlogf(pr[i], tab) : 0.0f;
-        const float diff = fabsf(surprisal - entropy);
-        sk[i] = ((uint64_t)f2ord(diff) << 32) | i;  // ascending score, then position
-      }
-      if (l == 0) sk[len] = ~0ull;  // pad for the pairwise reads below
       wave_sync();
-      for (uint32_t g = 0; g < len; g += 256) {
-        uint64_t mine[4];
-        uint32_t rank[4];
+      // scores (ascending score, then position), over the entropy terms
+      uint32_t* d = (uint32_t*)bf.aux;
+      uint64_t mn = ~0ull;
+      for (uint32_t i = l; i < len; i += 64) {
+        const float surprisal = pr[i] > 0.0f ? -lg[i] : 0.0f;
+        const uint32_t sc = f2ord(fabsf(surprisal - entropy));
+        d[i] = sc;
+        const uint64_t k = ((uint64_t)sc << 32) | i;
+        mn = k < mn ? k : mn;
+      }
+      wave_sync();
+      const uint32_t m = (uint32_t)wave_min_u64(mn);  // the first smallest score
+      bool v_shaped = true;
+      for (uint32_t i = l; i + 1 < len; i += 64) {
+        const uint32_t a = d[i], b = d[i + 1];
+        if (i + 1 < m ? a < b : (i >= m && a > b)) v_shaped = false;
+      }
+      if (__ballot(!v_shaped) == 0) {
+        typical_rank_v(ids, pr, d, len, m, bf.ids_b, bf.pr_b);
+      } else {  // any other shape: each key ranked against every key
+        uint64_t* sk = bf.aux64;
+        for (uint32_t i = l; i < len; i += 64) sk[i] = ((uint64_t)d[i] << 32) | i;
+        if (l == 0) sk[len] = ~0ull;  // pad for the pairwise reads below
+        wave_sync();
+        for (uint32_t g = 0; g < len; g += 256) {
+          uint64_t mine[4];
+          uint32_t rank[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const uint32_t i = g + l + 64u * t;
-          mine[t] = i < len ? sk[i] : 0ull;
-          rank[t] = 0;
-        }
-        for (uint32_t j = 0; j < len; j += 2) {
-          const uint64_t a0 = sk[j], a1 = sk[j + 1];
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t i = g + l + 64u * t;
+            mine[t] = i < len ? sk[i] : 0ull;
+            rank[t] = 0;
+          }
+          for (uint32_t j = 0; j < len; j += 2) {
+            const uint64_t a0 = sk[j], a1 = sk[j + 1];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) rank[t] += (a0 < mine[t] ? 1u : 0u) + (a1 < mine[t] ? 1u : 0u);
-        }
+            for (int t = 0; t < 4; ++t) rank[t] += (a0 < mine[t] ? 1u : 0u) + (a1 < mine[t] ? 1u : 0u);
+          }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const uint32_t i = g + l + 64u * t;
-          if (i < len) {
-            bf.ids_b[rank[t]] = ids[i];
-            bf.pr_b[rank[t]] = pr[i];
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t i = g + l + 64u * t;
+            if (i < len) {
+              bf.ids_b[rank[t]] = ids[i];
+              bf.pr_b[rank[t]] = pr[i];
+            }
           }
         }
       }
