@@ -51,7 +51,10 @@ extern "C" {
 #define OXS_ROW_OK 0            /* Ok(token); token recorded (sampler.rs:387) */
 #define OXS_ROW_EMPTY 1         /* every logit -inf or NaN: Ok(0), nothing recorded (sampler.rs:267-270) */
 #define OXS_ROW_HISTORY_FULL 2  /* Ok(token), but the device history had no room to record it */
-#define OXS_ROW_UNSUPPORTED 3   /* the row asks for a stage this build does not run on the GPU; token 0 */
+#define OXS_ROW_UNSUPPORTED 3   /* the row needs more than the sampler was sized for: a pool max(top_k, 256)
+                                   (at most V) above oxs_limits.max_top_k, or a DRY pass penalising more
+                                   distinct ids than a row's DRY list holds (8192; 2048 through
+                                   oxs_sample_batch_static); token 0 */
 #define OXS_ROW_MISSING_STATE 4 /* a Mirostat row but oxs_batch.mirostat_mu is NULL; token 0 */
 
 /* MirostatMode, sampler.rs:77-82. */
@@ -111,7 +114,8 @@ typedef struct oxs_sampling_config {
 typedef struct oxs_limits {
   uint32_t max_batch;  /* rows per call */
   uint32_t max_vocab;  /* V per row */
-  uint32_t max_top_k;  /* largest top_k any row may use; 0 means 256 */
+  uint32_t max_top_k;  /* largest top_k any row may use; 0 means 256. Above 1024 the sampler also
+                          holds [max_batch] x ~36 bytes x max_top_k of workspace for those rows */
 } oxs_limits;
 
 /*
@@ -243,7 +247,7 @@ int oxs_sample_batch(oxs_sampler* sampler, const oxs_batch* batch, void* stream)
 /*
  * oxs_sample_batch without a sampler and without any allocation: the same
  * kernels and results, with the workspace in a fixed device array of this
- * library (one per GPU, about 11 MiB, held until the process ends) instead
+ * library (one per GPU, about 13 MiB, held until the process ends) instead
  * of a sampler's. It has no counterpart in the reference; it is for callers
  * that cannot allocate device memory: code under HIP graph capture, serving
  * loops and harnesses that forbid hipMalloc.

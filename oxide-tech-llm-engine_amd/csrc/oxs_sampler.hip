@@ -51,8 +51,10 @@ constexpr int kMaxChunk = 8192;   // logits per stream block
 constexpr int kMaxChunks = 64;    // chunks per row
 constexpr int kBuckets = 256;     // tail counting-sort buckets
 constexpr int kRecPer = kMaxChunks * kWavesPerBlock / 64;  // wavefront records per lane a tail wavefront reads
-constexpr int kDryMax = 1024;      // longest DRY history slice run on the device (sampler.rs:395)
-constexpr int kDryHash = 2048;     // DRY id hash slots
+constexpr int kDryMax = 1024;      // longest DRY history slice copied into LDS (longer ones are read in place)
+constexpr int kDryHash = 2048;     // DRY id hash slots in LDS (slices of up to kDryMax ids)
+constexpr int kDryList = kDryHash;  // entries of a row's DRY list without a global DRY hash (the static workspace)
+constexpr int kDryListBig = 8192;   // ... with one: the most distinct ids a longer slice may penalise
 constexpr int kHistUnroll = 4;    // history-window ids per stream thread read with the logits
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -111,8 +113,10 @@ struct Params {
   uint64_t* wave_theta;  // [B][S*4] wavefront records: threshold << 32 | largest key
   uint32_t* wave_count;  // [B][S*4]
   const uint64_t* libm;  // [kLibmWords]: the libm tables (exp2, 1/c, ln c, log2 c) as bit patterns
-  uint64_t* dry_list;    // [B][kDryMax]: DRY rows' (id << 32 | value bits), sorted by id
+  uint64_t* dry_list;    // [B][dry_cap]: DRY rows' (id << 32 | value bits), sorted by id
   uint32_t* dry_count;   // [B]
+  uint32_t* dry_ghash;   // [B][3][2 * dry_cap] id, count and value slots for slices past kDryMax, or NULL
+  uint32_t dry_cap;      // a row's DRY list entries (a power of two)
   // decode step (kFlagDecode): the decode loop's per-row state and host outputs
   uint32_t* dec_token;    // [B] next step's input token
   int32_t* dec_pos;       // [B] position
@@ -120,6 +124,12 @@ struct Params {
   uint64_t* host_tokens;  // [B] host memory: (row's step count << 32) | token
   uint32_t* row_steps;    // [B] workspace: decode steps each row has handed to the host
   uint32_t* path_counts;  // [kPathKinds] workspace, or NULL: rows per top-M selection path
+  // rows whose M = max(top_k, 256) exceeds kMaxM (the wide kernel), or NULL
+  uint64_t* wide_keys;  // [B][wide_n2] a row's top-M keys, then sorted
+  uint32_t* wide_arr;   // [B][7 * wide_ld] the chain's arrays of such a row
+  uint32_t wide_cap;    // the largest M run (the sampler's max_top_k)
+  uint32_t wide_n2;     // a power of two >= wide_cap
+  uint32_t wide_ld;     // >= wide_cap + 16, a multiple of 4
 };
 
 // ---------------------------------------------------------------- keys
@@ -828,6 +838,7 @@ struct TailShared {
   uint64_t a_kmin[kWavesPerBlock];  // per-wavefront smallest valid keys
   uint32_t scan_scratch[8];
   uint32_t sel_digit, sel_above, sel_count, counter;
+  uint32_t dry_full;  // the DRY pass found more distinct ids than its hash holds
 };
 
 // Sorts n keys in LDS descending (ascending if ASC), padding to a power of two.
@@ -855,6 +866,57 @@ __device__ void bitonic_sort(uint64_t* a, uint32_t n) {
       }
       __syncthreads();
     }
+  }
+}
+
+// One compare-exchange of the bitonic network that sorts descending: entry i
+// against i ^ j (> i) at merge size k (as bitonic_sort<false>).
+__device__ __forceinline__ void bitonic_cx(uint64_t* a, uint32_t la, uint32_t i, uint32_t j, uint32_t k) {
+  const uint32_t lb = la ^ j;
+  const uint64_t x = a[la], y = a[lb];
+  const bool swap = (i & k) ? (x > y) : (x < y);
+  if (swap) {
+    a[la] = y;
+    a[lb] = x;
+  }
+}
+
+// The steps j = j0, j0 / 2, ..., 1 of merge size k on the tile of `tile_n`
+// entries of g starting at tb, in LDS (tile_n <= kTailArea).
+__device__ void bitonic_tile(uint64_t* g, uint32_t tb, uint32_t tile_n, uint32_t k, uint32_t j0, uint64_t* tile) {
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t i = tid; i < tile_n; i += kThreads) tile[i] = g[tb + i];
+  __syncthreads();
+  for (uint32_t kk = (k ? k : 2); kk <= (k ? k : tile_n); kk <<= 1) {
+    for (uint32_t j = (k ? j0 : kk >> 1); j > 0; j >>= 1) {
+      for (uint32_t li = tid; li < tile_n; li += kThreads)
+        if ((li ^ j) > li) bitonic_cx(tile, li, tb + li, j, kk);
+      __syncthreads();
+    }
+  }
+  for (uint32_t i = tid; i < tile_n; i += kThreads) g[tb + i] = tile[i];
+  __syncthreads();
+}
+
+// Sorts g[0 .. n) descending in global memory (g has room for the next power
+// of two of n, padded with zeros, which no key equals): the bitonic network,
+// with every step whose partner distance is below the LDS tile done on tiles
+// in LDS and only the longer ones as passes over global memory.
+__device__ void wide_sort(uint64_t* g, uint32_t n, uint64_t* tile) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (uint32_t i = n + tid; i < n2; i += kThreads) g[i] = 0ull;
+  __syncthreads();
+  const uint32_t T = min(n2, (uint32_t)kTailArea);
+  for (uint32_t tb = 0; tb < n2; tb += T) bitonic_tile(g, tb, T, 0u, 0u, tile);  // merge sizes 2 .. T
+  for (uint32_t k = 2 * T; k <= n2; k <<= 1) {
+    for (uint32_t j = k >> 1; j >= T; j >>= 1) {
+      for (uint32_t i = tid; i < n2; i += kThreads)
+        if ((i ^ j) > i) bitonic_cx(g, i, i, j, k);
+      __syncthreads();
+    }
+    for (uint32_t tb = 0; tb < n2; tb += T) bitonic_tile(g, tb, T, k, T >> 1, tile);
   }
 }
 
@@ -898,7 +960,7 @@ __device__ __forceinline__ void build_table(const Params& p, const RowXf& r, uin
   }
   if (tid == 0 && r.nl_active && r.nl_id >= c0 && r.nl_id < c1) atomicOr(&table[r.nl_id - c0], kNlFlag);
   if (r.dry) {
-    const uint64_t* dl = p.dry_list + (size_t)row * kDryMax;
+    const uint64_t* dl = p.dry_list + (size_t)row * p.dry_cap;
     const uint32_t nd = p.dry_count[row];
     for (uint32_t k = tid; k < nd; k += kThreads) {
       const uint32_t id = (uint32_t)(dl[k] >> 32);
@@ -910,7 +972,7 @@ __device__ __forceinline__ void build_table(const Params& p, const RowXf& r, uin
 
 // The DRY-stage value of id (the row's sorted DRY list holds it).
 __device__ __forceinline__ float dry_value(const Params& p, uint32_t row, uint32_t id) {
-  const uint64_t* dl = p.dry_list + (size_t)row * kDryMax;
+  const uint64_t* dl = p.dry_list + (size_t)row * p.dry_cap;
   uint32_t lo = 0, hi = p.dry_count[row];
   while (hi - lo > 1) {
     const uint32_t mid = (lo + hi) >> 1;
@@ -938,11 +1000,11 @@ __device__ __forceinline__ float transformed_logit(const Params& p, const RowXf&
 // Exact top-M of a whole row without the candidate sets: a radix select over
 // all V keys, re-reading the row once per digit. Used only when the candidate
 // keys cannot be proven to hold the row's top M. Writes the top min(M, pool)
-// keys to out (unordered); returns that count.
+// keys to out (unordered, at most `cap`: M <= cap); returns that count.
 template <int DT>
 __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowXf& r, uint32_t row, uint32_t M,
                                      uint32_t* table, uint32_t* hist, uint64_t* out,
-                                     TailShared& ts) {
+                                     TailShared& ts, uint32_t cap = kMaxM) {
   const uint32_t tid = threadIdx.x;
   uint64_t prefix = 0, mask = 0;
   uint32_t kk = 0, meff = 0;
@@ -995,7 +1057,7 @@ __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowX
       const uint64_t key = comp_key(k, i);
       if ((key & mask) >= prefix) {
         const uint32_t pos = atomicAdd(&ts.counter, 1u);
-        if (pos < (uint32_t)kMaxM) out[pos] = key;
+        if (pos < cap) out[pos] = key;
       }
     }
     __syncthreads();
@@ -1250,6 +1312,7 @@ struct ChainBufs {
   float* aux;
   uint64_t* aux64;
   float* hit;  // 16 floats
+  uint64_t* big;  // global scratch of a power of two >= n entries (wide rows), or NULL
 };
 
 
@@ -1329,6 +1392,38 @@ __device__ __forceinline__ void typical_rank_v(const uint32_t* ids, const float*
     }
     ids_b[rank] = ids[i];
     pr_b[rank] = pr[i];
+  }
+}
+
+// Typical's stable sort of a long list (wide rows) by one wavefront: keys
+// (d[i] << 32 | i) sorted ascending by a bitonic network in global memory
+// (sk: a power of two >= len entries), then (ids, pr) gathered in that order.
+__device__ void wave_sort_by_score(const uint32_t* ids, const float* pr, const uint32_t* d, uint32_t len,
+                                   uint64_t* sk, uint32_t* ids_b, float* pr_b) {
+  const uint32_t l = threadIdx.x & 63;
+  uint32_t n2 = 1;
+  while (n2 < len) n2 <<= 1;
+  for (uint32_t i = l; i < n2; i += 64) sk[i] = i < len ? ((uint64_t)d[i] << 32) | i : ~0ull;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");  // this wavefront's stores complete
+  for (uint32_t k = 2; k <= n2; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t i = l; i < n2; i += 64) {
+        const uint32_t ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t x = sk[i], y = sk[ixj];
+          if ((i & k) ? (x < y) : (x > y)) {
+            sk[i] = y;
+            sk[ixj] = x;
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    }
+  }
+  for (uint32_t r = l; r < len; r += 64) {
+    const uint32_t i = (uint32_t)sk[r];
+    ids_b[r] = ids[i];
+    pr_b[r] = pr[i];
   }
 }
 
@@ -1502,6 +1597,8 @@ __device__ __forceinline__ void wave_chain(const Params& p, const oxs_sampling_c
       }
       if (__ballot(!v_shaped) == 0) {
         typical_rank_v(ids, pr, d, len, m, bf.ids_b, bf.pr_b);
+      } else if (len > (uint32_t)kMaxM && bf.big) {  // any other shape, a long list: sorted
+        wave_sort_by_score(ids, pr, d, len, bf.big, bf.ids_b, bf.pr_b);
       } else {  // any other shape: each key ranked against every key
         uint64_t* sk = bf.aux64;
         for (uint32_t i = l; i < len; i += 64) sk[i] = ((uint64_t)d[i] << 32) | i;
@@ -1644,21 +1741,36 @@ __device__ __forceinline__ float pre_stages_of(const Params& p, const RowXf& r, 
 // penalties one rounded subtraction at a time in the reference's order
 // (longer matches first; the penalties of one length are equal, so their order
 // inside a length does not matter). The ids and values go to the row's list,
-// sorted by id. Uses the first 28 KB of `lds`.
+// sorted by id. A slice of up to kDryMax ids is copied into LDS and its ids
+// counted in an LDS hash (kDryHash slots: room for every id of the slice); a
+// longer one is read where it lies and counted in the row's global hash
+// (2 * dry_cap slots) when the workspace has one, else in the LDS hash.
+// Returns false (the row cannot be run) when the penalised ids outnumber what
+// the hash or the list holds. Uses the first 32 KB of `lds`.
 template <int DT>
-__device__ __forceinline__ void dry_pass(const Params& p, const RowXf& r, uint32_t row, uint32_t* lds,
+__device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32_t row, uint32_t* lds,
                                          const LibmTables& tab, TailShared& ts) {
   const uint32_t tid = threadIdx.x;
-  const uint32_t L = min(r.hlen, r.dry_range);  // :394-396; the caller checked L <= kDryMax
-  uint32_t* slice = lds;                         // [kDryMax]
-  uint32_t* hkey = slice + kDryMax;              // [kDryHash] ids (kEmptySlot: free)
-  uint32_t* cnt = hkey + kDryHash;               // [kDryHash] matches at the current length
-  float* val = (float*)(cnt + kDryHash);         // [kDryHash] values
+  const uint32_t L = min(r.hlen, r.dry_range);  // :394-396
   const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
-  for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
-  for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+  const bool in_lds = L <= (uint32_t)kDryMax;
+  const bool global = !in_lds && p.dry_ghash;
+  const uint32_t slots = global ? 2u * p.dry_cap : (uint32_t)kDryHash;  // a power of two
+  const uint32_t shift = 32u - (31u - __builtin_clz(slots));
+  uint32_t* slice = lds;  // [kDryMax]
+  uint32_t* hkey = global ? p.dry_ghash + (size_t)row * 3 * slots : slice + kDryMax;  // ids (kEmptySlot: free)
+  uint32_t* cnt = hkey + slots;                // matches at the current length
+  float* val = (float*)(cnt + slots);          // values
+  if (in_lds)
+    for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
+  const uint32_t* sl = in_lds ? (const uint32_t*)slice : hs;
+  for (uint32_t h = tid; h < slots; h += kThreads) {
     hkey[h] = kEmptySlot;
     cnt[h] = 0;
+  }
+  if (tid == 0) {
+    ts.dry_full = 0;
+    ts.counter = 0;
   }
   __syncthreads();
   const int allowed = (int)min(r.dry_allowed, 33u);
@@ -1667,29 +1779,33 @@ __device__ __forceinline__ void dry_pass(const Params& p, const RowXf& r, uint32
     const uint32_t n = L - (uint32_t)ml;
     for (uint32_t i = tid; i < n; i += kThreads) {
       bool m = true;
-      for (int t = 0; t < ml && m; ++t) m = slice[i + t] == slice[L - ml + t];
+      for (int t = 0; t < ml && m; ++t) m = sl[i + t] == sl[L - ml + t];
       if (!m) continue;
-      const uint32_t next = slice[i + ml];
+      const uint32_t next = sl[i + ml];
       if (next >= p.V) continue;  // logits.get_mut(next) is None
-      uint32_t h = (next * 0x9e3779b1u) >> 21;
-      for (int probe = 0; probe < kDryHash; ++probe) {  // at most L <= kDryHash / 2 distinct ids
+      uint32_t h = (next * 0x9e3779b1u) >> shift;
+      bool placed = false;
+      for (uint32_t probe = 0; probe < slots; ++probe) {
         const uint32_t prev = atomicCAS(&hkey[h], kEmptySlot, next);
         if (prev == kEmptySlot) {  // first sight: the value before DRY
           float x = load_logit<DT>(p, row, next);
           if (p.mask && !mask_allows(p, row, next)) x = neg_inf();
           val[h] = pre_stages_of(p, r, next, x);
+          if (atomicAdd(&ts.counter, 1u) >= p.dry_cap) ts.dry_full = 1;  // more ids than the list holds
         }
         if (prev == kEmptySlot || prev == next) {
           atomicAdd(&cnt[h], 1u);
+          placed = true;
           break;
         }
-        h = (h + 1) & (kDryHash - 1);
+        h = (h + 1) & (slots - 1);
       }
+      if (!placed) ts.dry_full = 1;  // every slot holds another id
     }
     __syncthreads();
     const float exponent = (float)(ml - allowed);
     const float pen = r.dry_mult * dpowf(r.dry_base, exponent, tab);  // :408-409
-    for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+    for (uint32_t h = tid; h < slots; h += kThreads) {
       const uint32_t k = cnt[h];
       if (k) {
         float v = val[h];
@@ -1700,20 +1816,46 @@ __device__ __forceinline__ void dry_pass(const Params& p, const RowXf& r, uint32
     }
     __syncthreads();
   }
-  uint64_t* keys = (uint64_t*)cnt;  // [kDryMax] (id << 32 | value bits), in the cleared counters
+  if (ts.dry_full) return false;  // (read after the barrier that ends the last length)
+  uint64_t* dl = p.dry_list + (size_t)row * p.dry_cap;
   if (tid == 0) ts.counter = 0;
   __syncthreads();
-  for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
-    const uint32_t id = hkey[h];
-    if (id != kEmptySlot) keys[atomicAdd(&ts.counter, 1u)] = ((uint64_t)id << 32) | __float_as_uint(val[h]);
+  uint32_t nd;
+  if (global) {  // the list in place, sorted in global memory
+    for (uint32_t h = tid; h < slots; h += kThreads) {
+      const uint32_t id = hkey[h];
+      if (id != kEmptySlot) dl[atomicAdd(&ts.counter, 1u)] = ((uint64_t)id << 32) | __float_as_uint(val[h]);
+    }
+    __syncthreads();
+    nd = ts.counter;
+    // ascending by id: sorted descending on the complemented ids, then complemented back
+    for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = ~dl[i];
+    wide_sort(dl, nd, (uint64_t*)lds);
+    for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = ~dl[i];
+  } else {  // (id << 32 | value bits) from the LDS table into registers, then over the start of `lds`
+    constexpr int kPerT = kDryHash / kThreads;
+    uint64_t mine[kPerT];
+    uint32_t held = 0;  // bit q: slot tid + q * kThreads holds an id
+#pragma unroll
+    for (int q = 0; q < kPerT; ++q) {
+      const uint32_t h = tid + q * kThreads;
+      const uint32_t id = hkey[h];
+      mine[q] = ((uint64_t)id << 32) | __float_as_uint(val[h]);
+      if (id != kEmptySlot) held |= 1u << q;
+    }
+    __syncthreads();
+    uint64_t* keys = (uint64_t*)lds;  // [kDryHash]
+#pragma unroll
+    for (int q = 0; q < kPerT; ++q)
+      if ((held >> q) & 1u) keys[atomicAdd(&ts.counter, 1u)] = mine[q];
+    __syncthreads();
+    nd = ts.counter;
+    bitonic_sort<true>(keys, nd);
+    for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = keys[i];
   }
-  __syncthreads();
-  const uint32_t nd = ts.counter;
-  bitonic_sort<true>(keys, nd);
-  uint64_t* dl = p.dry_list + (size_t)row * kDryMax;
-  for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = keys[i];
   if (tid == 0) p.dry_count[row] = nd;
   __syncthreads();
+  return true;
 }
 
 // ---------------------------------------------------------------- tail kernel
@@ -1804,8 +1946,10 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   for (uint32_t i = tid; i < (uint32_t)kBuckets + 64; i += kThreads) s_bcount[i] = 0;
 
 
-  const uint32_t M = max(c.top_k, 256u);
-  if (M > (uint32_t)kMaxM || (r.dry && min(r.hlen, r.dry_range) > (uint32_t)kDryMax)) {
+  // the pool size, at most V (filter_k = min(max(top_k, 256), len), sampler.rs:274)
+  const uint32_t M = min(max(c.top_k, 256u), max(p.V, 256u));
+  if (M > (uint32_t)kMaxM) {
+    if (p.wide_keys && M <= p.wide_cap) return;  // the wide kernel's row
     count_path(p, kPathNone);
     write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // sizes this build does not run on the device
     return;
@@ -1817,7 +1961,11 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   }
   // DRY rows: their values, then the exact path (the stream kernel's
   // candidates do not include DRY)
-  if (r.dry) dry_pass<DT>(p, r, row, (uint32_t*)s_keys, s_tab, ts);
+  if (r.dry && !dry_pass<DT>(p, r, row, (uint32_t*)s_keys, s_tab, ts)) {
+    count_path(p, kPathNone);
+    write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // more penalised ids than the DRY hash holds
+    return;
+  }
 
   // 2. the largest wavefront threshold and the largest key, from the
   // wavefront records, reduced by every wavefront on its own (a record of all
@@ -1977,6 +2125,78 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   bf.aux = (float*)(scratch + 2 * kChainLd);
   bf.aux64 = (uint64_t*)(scratch + 3 * kChainLd);
   bf.hit = s_hit;
+  bf.big = nullptr;
+  wave_chain<DT>(p, c, row, meff, bf, rs, s_tab);
+}
+
+// ---------------------------------------------------------------- wide rows
+
+// Rows whose top-M pool exceeds kMaxM (top_k > 1024), one block per row,
+// launched after the tail kernel (which leaves these rows alone) when the
+// sampler was created with max_top_k > 1024: the exact top-M radix select
+// into global memory, a sort there, and the same chain on arrays in global
+// memory. sampler.rs:272-279 (filter_k = max(top_k, 256) of the row, sorted).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void wide_kernel(const Params p) {
+  __shared__ __align__(16) uint64_t s_area[kTailArea];  // DRY pass, exact-path chunk table, sort tiles
+  __shared__ __align__(16) uint32_t s_hist[kBuckets + 64];
+  __shared__ __align__(16) float s_hit[16];
+  __shared__ TailShared ts;
+  __shared__ LibmTables s_tab;
+  const uint32_t row = blockIdx.x;
+  const uint32_t tid = threadIdx.x;
+  const LibmEntries tabv = fetch_libm_tables(p.libm);
+  const RowIn rin = load_row_in(p, row);
+  const oxs_sampling_config c = rin.cfg;
+  const uint32_t M = min(max(c.top_k, 256u), max(p.V, 256u));
+  if (M <= (uint32_t)kMaxM || M > p.wide_cap) return;  // (uniform: the tail kernel's rows)
+  const RowXf r = make_row_xf_h(p, c, rin.history_len);
+  RowState rs;
+  rs.uniform = rin.uniform;
+  rs.mu = rin.mu;
+  rs.rng = rin.rng;
+  rs.history_len = rin.history_len;
+  rs.raw = rin.raw;
+  rs.dec_pos = 0;
+  rs.dec_count = 0;
+  rs.dec_steps = 0;
+  if constexpr (kind_decode(DT)) {
+    if (p.dec_pos) rs.dec_pos = p.dec_pos[row];
+    if (p.dec_count) rs.dec_count = p.dec_count[row];
+    if (p.host_tokens) rs.dec_steps = p.row_steps[row];
+  }
+  store_libm_tables(tabv, s_tab);
+  __syncthreads();
+  if (c.mirostat_mode != OXS_MIROSTAT_DISABLED && !p.mu) {
+    count_path(p, kPathNone);
+    write_row_result<DT>(p, row, 0u, OXS_ROW_MISSING_STATE, rs);
+    return;
+  }
+  if (r.dry && !dry_pass<DT>(p, r, row, (uint32_t*)s_area, s_tab, ts)) {
+    count_path(p, kPathNone);
+    write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);
+    return;
+  }
+  count_path(p, kPathExact);
+  uint64_t* keys = p.wide_keys + (size_t)row * p.wide_n2;
+  const uint32_t meff = exact_select_row<DT>(p, r, row, M, (uint32_t*)s_area, s_hist, keys, ts, p.wide_cap);
+  if (meff == 0) {
+    write_row_result<DT>(p, row, 0u, OXS_ROW_EMPTY, rs);
+    return;
+  }
+  wide_sort(keys, meff, s_area);
+  uint32_t* arr = p.wide_arr + (size_t)row * 7 * p.wide_ld;
+  ChainBufs bf;
+  bf.ids = arr;
+  bf.pr = (float*)(arr + p.wide_ld);
+  bf.ids_b = arr + 2 * p.wide_ld;
+  bf.pr_b = (float*)(arr + 3 * p.wide_ld);
+  bf.aux = (float*)(arr + 4 * p.wide_ld);
+  bf.aux64 = (uint64_t*)(arr + 5 * p.wide_ld);  // [5 ld, 7 ld)
+  bf.hit = s_hit;
+  bf.big = keys;  // free once the chain arrays are written
+  keys_to_chain(keys, meff, bf.ids, bf.pr, s_tab);
+  if (tid >= 64) return;
   wave_chain<DT>(p, c, row, meff, bf, rs, s_tab);
 }
 
@@ -2126,6 +2346,7 @@ static hipError_t launch_all(int slots, bool vec, bool mask, const Params& p, ui
     hipLaunchKernelGGL((tail_kernel<KIND, kPer>), dim3(grid_b), dim3(kThreads), 0, st, (const uint64_t*)p.wave_theta,
                        (const uint64_t*)p.lists, (const uint32_t*)p.wave_count, p.libm, p.S, p.cap_w, p.cap_shift,
                        p.rpx, p.B, p);
+  if (p.wide_keys) hipLaunchKernelGGL((wide_kernel<KIND>), dim3(p.B), dim3(kThreads), 0, st, p);
   return hipGetLastError();
 }
 
@@ -2158,8 +2379,12 @@ struct oxs_sampler {
   uint64_t* libm;
   uint64_t* dry_list;
   uint32_t* dry_count;
+  uint32_t* dry_ghash;  // [max_batch][3][2 * kDryListBig]
   uint32_t* row_steps;  // [max_batch] decode steps each row has handed to the host
   uint32_t* path_counts;  // [kPathKinds] rows per top-M selection path
+  uint64_t* wide_keys;    // rows with top_k > 1024 (max_top_k > 1024 only), else NULL
+  uint32_t* wide_arr;
+  uint32_t wide_n2, wide_ld;
   bool count_paths;
   size_t bytes;
 };
@@ -2175,10 +2400,15 @@ struct Workspace {
   uint64_t* wave_theta;   // [max_batch][kMaxChunks * kWavesPerBlock]
   uint32_t* wave_count;   // [max_batch][kMaxChunks * kWavesPerBlock]
   uint64_t* libm;         // [kLibmWords]
-  uint64_t* dry_list;     // [max_batch][kDryMax]
+  uint64_t* dry_list;     // [max_batch][dry_cap]
   uint32_t* dry_count;    // [max_batch]
+  uint32_t* dry_ghash;    // [max_batch][3][2 * dry_cap], or null: DRY slices past kDryMax use the LDS hash
+  uint32_t dry_cap;
   uint32_t* row_steps;    // [max_batch] (decode steps only; may be null otherwise)
   uint32_t* path_counts;  // [kPathKinds] or null (counting off)
+  uint64_t* wide_keys;    // [max_batch][wide_n2] or null: rows with max(top_k, 256) > kMaxM are then unsupported
+  uint32_t* wide_arr;     // [max_batch][7 * wide_ld]
+  uint32_t wide_cap, wide_n2, wide_ld;
 };
 
 __device__ __forceinline__ uint64_t libm_word(uint32_t i) {  // the workspace's libm layout
@@ -2204,8 +2434,8 @@ constexpr size_t kStaticB = OXS_STATIC_MAX_BATCH;
 constexpr size_t kStaticW = (size_t)kMaxChunks * kWavesPerBlock;  // wavefront records per row
 constexpr size_t kStOffLists = 0;                                         // u64 [B][kUnionBig]
 constexpr size_t kStOffTheta = kStOffLists + kStaticB * kUnionBig;        // u64 [B][W]
-constexpr size_t kStOffDry = kStOffTheta + kStaticB * kStaticW;           // u64 [B][kDryMax]
-constexpr size_t kStOffLibm = kStOffDry + kStaticB * kDryMax;             // u64 [kLibmWords]
+constexpr size_t kStOffDry = kStOffTheta + kStaticB * kStaticW;           // u64 [B][kDryList]
+constexpr size_t kStOffLibm = kStOffDry + kStaticB * kDryList;            // u64 [kLibmWords]
 constexpr size_t kStOffCount = kStOffLibm + (size_t)kLibmWords;           // u32 [B][W]
 constexpr size_t kStOffDryCount = kStOffCount + kStaticB * kStaticW / 2;  // u32 [B]
 constexpr size_t kStaticWords = kStOffDryCount + kStaticB / 2;
@@ -2232,8 +2462,13 @@ static Workspace static_workspace(uint64_t* base) {
   w.libm = base + kStOffLibm;
   w.dry_list = base + kStOffDry;
   w.dry_count = (uint32_t*)(base + kStOffDryCount);
+  w.dry_ghash = nullptr;
+  w.dry_cap = kDryList;
   w.row_steps = nullptr;
   w.path_counts = nullptr;
+  w.wide_keys = nullptr;
+  w.wide_arr = nullptr;
+  w.wide_cap = w.wide_n2 = w.wide_ld = 0;
   return w;
 }
 
@@ -2249,8 +2484,15 @@ static oxs::Workspace sampler_workspace(const oxs_sampler* s) {
   w.libm = s->libm;
   w.dry_list = s->dry_list;
   w.dry_count = s->dry_count;
+  w.dry_ghash = s->dry_ghash;
+  w.dry_cap = oxs::kDryListBig;
   w.row_steps = s->row_steps;
   w.path_counts = s->count_paths ? s->path_counts : nullptr;
+  w.wide_keys = s->wide_keys;
+  w.wide_arr = s->wide_arr;
+  w.wide_cap = s->limits.max_top_k;
+  w.wide_n2 = s->wide_n2;
+  w.wide_ld = s->wide_ld;
   return w;
 }
 
@@ -2312,8 +2554,8 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return OXS_ERR_NO_DEVICE;
   if (device < 0 || device >= ndev) return OXS_ERR_INVALID_ARGUMENT;
-  const uint32_t mtk = limits->max_top_k ? limits->max_top_k : 256u;
-  if (mtk > (uint32_t)oxs::kMaxM) return OXS_ERR_LIMITS;
+  // a pool never holds more than V keys (filter_k = min(max(top_k, 256), len), sampler.rs:274)
+  const uint32_t mtk = min(limits->max_top_k ? limits->max_top_k : 256u, max(limits->max_vocab, 256u));
   if ((uint64_t)limits->max_vocab > (uint64_t)oxs::kMaxChunks * oxs::kMaxChunk) return OXS_ERR_LIMITS;
   if (hipSetDevice(device) != hipSuccess) return OXS_ERR_HIP;
   oxs_sampler* s = (oxs_sampler*)calloc(1, sizeof(oxs_sampler));
@@ -2333,14 +2575,27 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
                   hipMalloc((void**)&s->wave_theta, b_theta) == hipSuccess &&
                   hipMalloc((void**)&s->wave_count, b_count) == hipSuccess &&
                   hipMalloc((void**)&s->libm, oxs::kLibmWords * sizeof(uint64_t)) == hipSuccess &&
-                  hipMalloc((void**)&s->dry_list, B * oxs::kDryMax * sizeof(uint64_t)) == hipSuccess &&
+                  hipMalloc((void**)&s->dry_list, B * oxs::kDryListBig * sizeof(uint64_t)) == hipSuccess &&
+                  hipMalloc((void**)&s->dry_ghash, B * 6 * oxs::kDryListBig * sizeof(uint32_t)) == hipSuccess &&
                   hipMalloc((void**)&s->dry_count, B * sizeof(uint32_t)) == hipSuccess &&
                   hipMalloc((void**)&s->row_steps, B * sizeof(uint32_t)) == hipSuccess &&
                   hipMemset(s->row_steps, 0, B * sizeof(uint32_t)) == hipSuccess &&
                   hipMalloc((void**)&s->path_counts, oxs::kPathKinds * sizeof(uint32_t)) == hipSuccess &&
                   hipMemset(s->path_counts, 0, oxs::kPathKinds * sizeof(uint32_t)) == hipSuccess;
+  size_t b_wide = 0;
+  if (ok && mtk > (uint32_t)oxs::kMaxM) {  // rows with top_k > 1024: the wide kernel's workspace
+    uint32_t n2 = 1;
+    while (n2 < mtk) n2 <<= 1;
+    s->wide_n2 = n2;
+    s->wide_ld = (mtk + 16u + 3u) & ~3u;
+    const size_t b_wk = B * (size_t)n2 * sizeof(uint64_t), b_wa = B * 7 * (size_t)s->wide_ld * sizeof(uint32_t);
+    ok = hipMalloc((void**)&s->wide_keys, b_wk) == hipSuccess && hipMalloc((void**)&s->wide_arr, b_wa) == hipSuccess;
+    b_wide = b_wk + b_wa;
+  }
   s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t) +
-             B * (oxs::kDryMax * sizeof(uint64_t) + 2 * sizeof(uint32_t)) + oxs::kPathKinds * sizeof(uint32_t);
+             B * (oxs::kDryListBig * (sizeof(uint64_t) + 6 * sizeof(uint32_t)) + 2 * sizeof(uint32_t)) +
+             oxs::kPathKinds * sizeof(uint32_t) +
+             b_wide;
   if (ok) {  // the libm tables, as bit patterns, in the workspace
     uint64_t host[oxs::kLibmWords];
     ok = hipMemcpyFromSymbol(host, HIP_SYMBOL(oxs_libm::kExp2Tab), 32 * sizeof(uint64_t)) == hipSuccess &&
@@ -2365,8 +2620,11 @@ int oxs_sampler_destroy(oxs_sampler* s) {
   if (s->libm) (void)hipFree(s->libm);
   if (s->dry_list) (void)hipFree(s->dry_list);
   if (s->dry_count) (void)hipFree(s->dry_count);
+  if (s->dry_ghash) (void)hipFree(s->dry_ghash);
   if (s->row_steps) (void)hipFree(s->row_steps);
   if (s->path_counts) (void)hipFree(s->path_counts);
+  if (s->wide_keys) (void)hipFree(s->wide_keys);
+  if (s->wide_arr) (void)hipFree(s->wide_arr);
   free(s);
   return OXS_OK;
 }
@@ -2467,7 +2725,14 @@ static int sample_impl(const oxs::Workspace& ws, const oxs_batch* b, const oxs_d
   p.libm = ws.libm;
   p.dry_list = ws.dry_list;
   p.dry_count = ws.dry_count;
+  p.dry_ghash = ws.dry_ghash;
+  p.dry_cap = ws.dry_cap;
   p.path_counts = ws.path_counts;
+  p.wide_keys = ws.wide_keys;
+  p.wide_arr = ws.wide_arr;
+  p.wide_cap = ws.wide_cap;
+  p.wide_n2 = ws.wide_n2;
+  p.wide_ld = ws.wide_ld;
   if (io) {
     if (!ws.row_steps) return OXS_ERR_INVALID_ARGUMENT;
     p.flags |= kFlagDecode;

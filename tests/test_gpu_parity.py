@@ -162,6 +162,131 @@ def test_mixed_configs_ragged_vocab(torch_gpu, V):
             run_oracle(w, kept_ld=1024, logits_out=True), RTOL_F32, f"mixed V={V}")
 
 
+def wide_workload(B, V, seed, dtype="f32"):
+    """Rows whose pool max(top_k, 256) exceeds 1024 (the wide kernel), among ordinary rows."""
+    from oxide_sampler import SamplingConfig
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    x[:, rng.choice(V, 30, replace=False)] += 5.0
+    if V > 3000:
+        x[:, 2000:2600] = np.float32(0.75)  # equal values inside the pool: the lower id ranks first
+    logits = wl.f32_to_bf16_bits(x) if dtype == "bf16" else x
+    ks = [1025, 2000, 50000, 40, 0, 1100]
+    base = [
+        dict(temperature=0.8),
+        dict(temperature=1.1, top_p=0.999, min_p=0.0001),
+        dict(temperature=1.3, tfs_z=0.99, typical_p=0.99),
+        dict(temperature=0.7, xtc_threshold=0.001, xtc_probability=1.0, top_p=0.95),
+        dict(mirostat_mode=MirostatMode.V2, mirostat_tau=9.0, mirostat_eta=0.1),
+        dict(mirostat_mode=MirostatMode.V1, mirostat_tau=8.0, mirostat_eta=0.2),
+        dict(temperature=0.9, dry_multiplier=0.8, dry_base=1.75, dry_allowed_length=2, dry_range=2048,
+             repeat_penalty=1.1, repeat_last_n=64, logit_biases={3: 2.0}, banned_tokens={5}),
+        dict(temperature=0.0),
+    ]
+    configs = []
+    for b in range(B):
+        kw = dict(base[b % len(base)])
+        kw["top_k"] = ks[b % len(ks)]
+        configs.append(wl.disabled_config(**kw) if b % 9 else SamplingConfig(top_k=kw["top_k"]))
+    cap = 3000
+    history = rng.integers(0, V, size=(B, cap), dtype=np.uint32)
+    hlen = rng.integers(0, 2900, size=B).astype(np.uint32)
+    for b in range(B):
+        n = int(hlen[b])
+        if n >= 40:
+            history[b, n - 40:n] = np.tile(rng.integers(0, V, size=5, dtype=np.uint32), 8)
+    return wl.Workload(name=f"wide top_k B={B} V={V}", logits=logits, dtype=dtype, configs=configs,
+                       history=history, history_len=hlen, uniforms=wl.xorshift_uniforms(B, seed),
+                       mu=np.full(B, 18.0, np.float32))
+
+
+@pytest.mark.parametrize("V,dtype", [(60000, "f32"), (151936, "bf16"), (1500, "f32")])
+def test_wide_top_k(torch_gpu, V, dtype):
+    # top_k 1025, 2000 and 50000 (kept to V when larger) beside ordinary rows: the wide kernel's
+    # exact top-M select, its sort in global memory and the chain over up to 50000 candidates
+    B = 24
+    w = wide_workload(B, V, seed=500 + V, dtype=dtype)
+    banner(f"wide top_k B={B} V={V} {dtype}")
+    compare(run_gpu(w, torch_gpu, kept_ld=2048, logits_out=True, max_top_k=50000),
+            run_oracle(w, kept_ld=2048, logits_out=True, n_threads=oracle_threads()),
+            RTOL_BF16 if dtype == "bf16" else RTOL_F32, f"wide V={V}")
+
+
+def test_wide_top_k_beyond_the_sampler_limit(torch_gpu):
+    # a sampler created with max_top_k = 2000 runs top_k 2000 and reports top_k 5000 unsupported
+    from harness import gpu_sampler
+    w = wide_workload(8, 60000, seed=77)
+    for b in range(8):
+        w.configs[b].top_k = 5000 if b == 2 else 2000
+    s = gpu_sampler(8, 60000, 2000, exact_limits=True)
+    assert s.limits[2] == 2000
+    banner("wide top_k beyond max_top_k")
+    g = run_gpu(w, torch_gpu, kept_ld=256, max_top_k=2000, exact_limits=True)
+    r = run_oracle(w, kept_ld=256)
+    assert g.status[2] == _abi.OXS_ROW_UNSUPPORTED and g.tokens[2] == 0
+    keep = np.arange(8) != 2
+    np.testing.assert_array_equal(g.tokens[keep], r.tokens[keep])
+    np.testing.assert_array_equal(g.kept_count[keep], r.kept_count[keep])
+
+
+def dry_long_workload(B, V, seed):
+    """DRY rows whose slices (1500 and 4096 ids) are longer than the 1024 ids the tail copies into LDS."""
+    rng = np.random.default_rng(seed)
+    logits = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    cap = 5000
+    history = rng.integers(0, V, size=(B, cap), dtype=np.uint32)
+    hlen = rng.integers(3000, 4900, size=B).astype(np.uint32)
+    for b in range(B):  # repeated motifs spread over the slice: matches of several lengths
+        n = int(hlen[b])
+        motif = rng.integers(0, V, size=int(rng.integers(3, 9)), dtype=np.uint32)
+        for start in rng.integers(0, n - 200, size=12):
+            history[b, start:start + 4 * len(motif)] = np.tile(motif, 4)
+        history[b, n - 2 * len(motif):n] = np.tile(motif, 2)
+    configs = [wl.disabled_config(temperature=0.9, dry_multiplier=float(rng.choice([0.5, 1.2])),
+                                  dry_base=1.75, dry_allowed_length=int(rng.choice([0, 2, 3])),
+                                  dry_range=int(rng.choice([1500, 4096])), top_k=int(rng.choice([0, 40])),
+                                  repeat_penalty=1.1, repeat_last_n=64)
+               for _ in range(B)]
+    return wl.Workload(name=f"dry long B={B} V={V}", logits=logits, dtype="f32", configs=configs,
+                       history=history, history_len=hlen, uniforms=wl.xorshift_uniforms(B, seed),
+                       mu=np.full(B, 10.0, np.float32))
+
+
+def test_dry_long_slices(torch_gpu):
+    w = dry_long_workload(24, 32000, seed=31)
+    banner("DRY slices of 1500 and 4096 ids B=24 V=32000")
+    compare(run_gpu(w, torch_gpu, kept_ld=256, logits_out=True), run_oracle(w, kept_ld=256, logits_out=True),
+            RTOL_F32, "dry long")
+
+
+def test_dry_more_penalised_ids_than_the_list_holds(torch_gpu):
+    # history [A, B, x_i] x 9000 with distinct x_i, ending in [A, B]: the length-2 suffix matches
+    # before every x_i, so 9000 distinct ids take a DRY penalty, more than a row's 8192-entry DRY
+    # list holds: that row reports OXS_ROW_UNSUPPORTED (token 0); the other rows are unaffected
+    V = 32000
+    w = dry_long_workload(8, V, seed=32)
+    a, b = 7, 11
+    xs = np.arange(100, 9100, dtype=np.uint32)
+    trip = np.stack([np.full(len(xs), a, np.uint32), np.full(len(xs), b, np.uint32), xs], axis=1).reshape(-1)
+    seq = np.concatenate([trip, np.array([a, b], np.uint32)])
+    hist = np.zeros((8, len(seq) + 100), np.uint32)
+    hist[:, :w.history.shape[1]] = w.history
+    hist[3, :len(seq)] = seq
+    w.history = hist
+    w.history_len = w.history_len.copy()
+    w.history_len[3] = len(seq)
+    w.configs[3] = wl.disabled_config(temperature=0.9, dry_multiplier=0.8, dry_base=1.75, dry_allowed_length=2,
+                                      dry_range=30000)
+    banner("DRY row with 9000 distinct penalised ids")
+    g = run_gpu(w, torch_gpu, kept_ld=256)
+    r = run_oracle(w, kept_ld=256)
+    assert g.status[3] == _abi.OXS_ROW_UNSUPPORTED and g.tokens[3] == 0
+    keep = np.arange(8) != 3
+    np.testing.assert_array_equal(g.tokens[keep], r.tokens[keep])
+    np.testing.assert_array_equal(g.status[keep], r.status[keep])
+    np.testing.assert_array_equal(g.history_len[keep], r.history_len[keep])
+
+
 def test_mixed_configs_device_rng(torch_gpu):
     # rng_state instead of uniforms: each drawing row advances its xorshift state by one step
     w = mixed_workload(40, 32000, seed=7)

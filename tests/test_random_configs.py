@@ -4,7 +4,9 @@ Each case draws a batch shape, a logits dtype (f32 or bf16), a logit
 distribution (Gaussian, heavy spikes, long runs of equal values, -inf rows), a
 grammar mask (none, per row or shared), a softcap, histories of random
 length, and for every row a SamplingConfig whose fields are each enabled with
-probability 1/2 at random values (sampler.rs:16-73). The HIP path must match
+probability 1/2 at random values (sampler.rs:16-73), top_k up to 50000 (the
+wide kernel past 1024), DRY ranges up to 4096
+over histories up to 4400 ids. The HIP path must match
 the oracle exactly: tokens, status, kept ids and probabilities, history, mu.
 `test_random_configs_large_vocab` draws vocabularies above 131072 (more than 16
 stream chunks per row, the 4096-key candidate union) with batches divisible by 8
@@ -30,7 +32,7 @@ def random_config(rng, V):
     coin = lambda: rng.random() < 0.5  # noqa: E731
     kw["temperature"] = float(rng.choice([0.0, 1e-7, 0.3, 0.7, 1.0, 1.6])) if coin() else 1.0
     if coin():
-        kw["top_k"] = int(rng.choice([1, 2, 40, 50, 255, 256, 300, 1024]))
+        kw["top_k"] = int(rng.choice([1, 2, 40, 50, 255, 256, 300, 1024, 2000, 50000]))
     if coin():
         kw["top_p"] = float(rng.choice([0.5, 0.9, 0.95, 0.999]))
     if coin():
@@ -50,7 +52,7 @@ def random_config(rng, V):
         kw["dry_multiplier"] = float(rng.choice([0.5, 1.5]))
         kw["dry_base"] = float(rng.choice([1.1, 1.75]))
         kw["dry_allowed_length"] = int(rng.choice([0, 2, 3]))
-        kw["dry_range"] = int(rng.choice([16, 128, 1024]))
+        kw["dry_range"] = int(rng.choice([16, 128, 1024, 4096]))
     if coin():
         kw["repeat_penalty"] = float(rng.choice([0.9, 1.1, 1.3]))
         kw["repeat_last_n"] = int(rng.choice([0, 8, 64, 512]))
@@ -87,10 +89,12 @@ def random_workload(seed, large_vocab=False):
         x[1, :] = -np.inf
     bf16 = rng.random() < 0.3
     logits = wl.f32_to_bf16_bits(x) if bf16 else x
-    cap = 1100
+    cap = 4500
     history = rng.integers(0, V, size=(B, cap), dtype=np.uint32)
     history[:, ::9] = np.uint32(min(10, V - 1))
     hlen = rng.integers(0, 1090, size=B).astype(np.uint32)
+    long_rows = rng.random(B) < 0.3  # DRY slices past the 1024 ids an LDS copy holds
+    hlen[long_rows] = rng.integers(1100, 4400, size=int(long_rows.sum())).astype(np.uint32)
     for b in range(B):
         n = int(hlen[b])
         if n >= 30 and rng.random() < 0.5:  # repeated motifs: DRY n-gram matches
@@ -117,7 +121,7 @@ def test_random_configs(torch_gpu, seed):
     w, shared = random_workload(1000 + seed)
     banner(f"{w.name} {w.dtype} mask={'shared' if shared else w.mask is not None} "
            f"softcap={w.extra.get('softcap', 0)}")
-    g = run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=1024, shared_mask=shared)
+    g = run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=50000, shared_mask=shared)
     r = run_oracle(w, kept_ld=1024, logits_out=True, shared_mask=shared)
     compare(g, r, RTOL_BF16 if w.dtype == "bf16" else RTOL_F32, w.name)
 
@@ -128,7 +132,7 @@ def test_random_configs_large_vocab(torch_gpu, seed):
     w, shared = random_workload(2000 + seed, large_vocab=True)
     banner(f"{w.name} {w.dtype} mask={'shared' if shared else w.mask is not None} "
            f"softcap={w.extra.get('softcap', 0)}")
-    g = run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=1024, shared_mask=shared)
+    g = run_gpu(w, torch_gpu, kept_ld=1024, logits_out=True, max_top_k=50000, shared_mask=shared)
     r = run_oracle(w, kept_ld=1024, logits_out=True, shared_mask=shared, n_threads=8)
     compare(g, r, RTOL_BF16 if w.dtype == "bf16" else RTOL_F32, w.name)
 
@@ -187,7 +191,7 @@ def test_random_decode_steps(torch_gpu, seed):
     lib = _abi.load_library()
     host = ctypes.c_void_p()
     _abi.check(lib.oxs_host_alloc(8 * B, ctypes.byref(host)), "oxs_host_alloc")
-    s = BatchSampler(B, V, 1024)
+    s = BatchSampler(B, V, 50000)  # rows with top_k > 1024 take the wide kernel's decode form
     try:
         io = OxsDecodeIo(d_dec["current_token"].data_ptr(), d_dec["current_position"].data_ptr(),
                          d_dec["generated_count"].data_ptr(), host.value)
