@@ -508,7 +508,7 @@ def config_pool(torch, w, n_pool, seed):
             x = torch.randn(B, V, device=d, generator=g) * 2.0
             spikes = torch.randint(0, V, (B, 5), device=d, generator=g)
             x.scatter_(1, spikes, 8.0)
-        elif w.name in ("config2", "config3"):
+        elif w.name in ("config2", "config3", "config2_dry"):
             x = torch.randn(B, V, device=d, generator=g) * 3.0
             x += prior[torch.argsort(torch.rand(B, V, device=d, generator=g), dim=1)]
         elif w.name == "config4":
@@ -543,7 +543,8 @@ def config_masks(torch, w, n_pool, seed):
 
 
 def bench_configs(args, torch):
-    """oxs_sample_batch on each of BASELINE.json's five configs. Each config
+    """oxs_sample_batch on each of BASELINE.json's five configs, and config 2
+    with DRY on every row (oxide_sampler.workloads.config2_dry). Each config
     rotates over its own pool of distinct input batches larger than twice the
     Infinity Cache (graph replays of the whole rotation), so every figure is
     streamed from HBM: us per call, rows/s, algorithmic GB/s with its roofline
@@ -553,8 +554,8 @@ def bench_configs(args, torch):
 
     d = torch.device("cuda")
     lines = {}
-    for cfg_id in (1, 2, 3, 4, 5):
-        w = wl.BUILDERS[cfg_id]()
+    for cfg_id in (1, 2, 3, 4, 5, "2dry"):
+        w = wl.config2_dry() if cfg_id == "2dry" else wl.BUILDERS[cfg_id]()
         name = w.name
         cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
         sampler = BatchSampler(w.batch, w.vocab, 256)
@@ -562,8 +563,9 @@ def bench_configs(args, torch):
         words = (w.vocab + 31) // 32 if w.mask is not None else 0
         batch_bytes = w.batch * (w.vocab * esz + words * 4)
         P = pool_batches(batch_bytes)
-        pool = config_pool(torch, w, P, 0x5EED0100 + cfg_id)
-        masks = config_masks(torch, w, P, 0x5EED0200 + cfg_id) if w.mask is not None else None
+        seed_id = 22 if cfg_id == "2dry" else cfg_id
+        pool = config_pool(torch, w, P, 0x5EED0100 + seed_id)
+        masks = config_masks(torch, w, P, 0x5EED0200 + seed_id) if w.mask is not None else None
         hist = torch.from_numpy(w.history.view(np.int32).copy()).to(d)
         hlen = torch.from_numpy(w.history_len.view(np.int32).copy()).to(d)
         mu = torch.from_numpy(w.mu.copy()).to(d) if w.mu is not None else None

@@ -839,6 +839,8 @@ struct TailShared {
   uint32_t scan_scratch[8];
   uint32_t sel_digit, sel_above, sel_count, counter;
   uint32_t dry_full;  // the DRY pass found more distinct ids than its hash holds
+  float dry_pen[33];  // DRY penalty per match length (dry_pass_lds)
+  uint32_t a_kmax[kWavesPerBlock];  // per-wavefront largest keys (DRY candidate rows)
 };
 
 // Sorts n keys in LDS descending (ascending if ASC), padding to a power of two.
@@ -1733,6 +1735,154 @@ __device__ __forceinline__ float pre_stages_of(const Params& p, const RowXf& r, 
   return special_pre(p.bias_ids, p.bias_values, r, x, e, id);
 }
 
+// LDS layout of the DRY pass over a slice of up to kDryMax ids (u32 offsets
+// into the tail's 32 KB area); the tail's DRY candidate step reads the hash.
+constexpr int kDrySlice = 0;                 // [kDryMax] the slice; then the occurrences sorted by slot
+constexpr int kDryKey = kDrySlice + kDryMax;  // [kDryHash] penalised ids (kEmptySlot: free)
+constexpr int kDryVal = kDryKey + kDryHash;   // [kDryHash] their values
+constexpr int kDryCnt = kDryVal + kDryHash;   // [kDryHash] occurrences per slot, then cursors; then the list
+constexpr int kDryOcc = kDryCnt + kDryHash;   // [kDryMax] (slot << 6 | match length) per penalising occurrence
+static_assert(kDryOcc + kDryMax <= 2 * kTailArea, "DRY LDS layout fits the tail area");
+
+// DRY (sampler.rs:393-415) over a slice of L <= kDryMax ids, in one pass
+// over the slice instead of one per match length. The occurrence at position
+// q (q < L) matches at length ml exactly when ml <= lambda(q), the length of
+// the longest common suffix of slice[..q) and the whole slice (at most 32 and
+// q): slice[q - ml .. q) == slice[L - ml .. L) holds for every shorter length
+// once it holds for one. So slice[q] takes one penalty per length in
+// [allowed, lambda(q)], and an id's value is its pre-stage value minus, for
+// ml = 32 down to allowed, pen(ml) once per occurrence with lambda >= ml, one
+// rounded subtraction at a time (the reference's order; the penalties of one
+// length are equal). The ids go into an LDS hash, each occurrence into a list
+// sorted by slot with a counting sort, and each slot's thread runs its id's
+// subtractions. Leaves the hash (ids, values) in LDS for dry_lookup.
+template <int DT>
+__device__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint32_t L, uint32_t* lds,
+                             const LibmTables& tab, TailShared& ts, uint64_t* dl) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t* slice = lds + kDrySlice;
+  uint32_t* hkey = lds + kDryKey;
+  float* val = (float*)(lds + kDryVal);
+  uint32_t* cnt = lds + kDryCnt;
+  uint32_t* occ = lds + kDryOcc;
+  const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
+  for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
+  for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+    hkey[h] = kEmptySlot;
+    cnt[h] = 0;
+  }
+  const uint32_t allowed = min(r.dry_allowed, 33u);
+  if (tid <= 32u && tid >= allowed)  // pen(ml), :408-409
+    ts.dry_pen[tid] = r.dry_mult * dpowf(r.dry_base, (float)(tid - allowed), tab);
+  if (tid == 0) ts.counter = 0;
+  __syncthreads();
+  for (uint32_t q = tid; q < L; q += kThreads) {
+    const uint32_t lim = min(q, 32u);
+    uint32_t k = 0;
+    while (k < lim && slice[q - 1 - k] == slice[L - 1 - k]) ++k;  // lambda(q)
+    const uint32_t next = slice[q];
+    if (k < allowed || next >= p.V) continue;  // no length in [allowed, k]; logits.get_mut(next) is None
+    uint32_t h = (next * 0x9e3779b1u) >> 21;
+    for (int probe = 0; probe < kDryHash; ++probe) {  // at most L <= kDryHash / 2 distinct ids
+      const uint32_t prev = atomicCAS(&hkey[h], kEmptySlot, next);
+      if (prev == kEmptySlot) {  // first sight: the value before DRY
+        float x = load_logit<DT>(p, row, next);
+        if (p.mask && !mask_allows(p, row, next)) x = neg_inf();
+        val[h] = pre_stages_of(p, r, next, x);
+      }
+      if (prev == kEmptySlot || prev == next) break;
+      h = (h + 1) & (kDryHash - 1);
+    }
+    atomicAdd(&cnt[h], 1u);
+    occ[atomicAdd(&ts.counter, 1u)] = (h << 6) | k;
+  }
+  __syncthreads();
+  // counting sort of the occurrences by slot: each thread owns slots tid + 256 j
+  constexpr int kPerT = kDryHash / kThreads;
+  uint32_t mine[kPerT], sum = 0;
+#pragma unroll
+  for (int j = 0; j < kPerT; ++j) {
+    mine[j] = cnt[tid + j * kThreads];
+    sum += mine[j];
+  }
+  uint32_t total;
+  const uint32_t start0 = block_excl_scan(sum, &total, ts.scan_scratch);
+  uint32_t start = start0;
+  // the slots of thread tid are not contiguous: a second pass gives each its start
+  // (slots in order tid, tid + 256, ...; their ranges in the sorted list follow that order)
+#pragma unroll
+  for (int j = 0; j < kPerT; ++j) {
+    cnt[tid + j * kThreads] = start;  // cursor
+    start += mine[j];
+  }
+  __syncthreads();
+  const uint32_t n_occ = ts.counter;
+  for (uint32_t o = tid; o < n_occ; o += kThreads) {
+    const uint32_t e = occ[o];
+    slice[atomicAdd(&cnt[e >> 6], 1u)] = e & 63u;  // the match lengths, grouped by slot
+  }
+  __syncthreads();
+  // each slot's id: its subtractions, longest match length first (the slot
+  // loop kept rolled: its body is long). A slot's occurrences end at its
+  // cursor and start at the previous slot's of this thread.
+  uint32_t prev_end = start0;
+#pragma unroll 1
+  for (int j = 0; j < kPerT; ++j) {
+    const uint32_t h = tid + j * kThreads;
+    const uint32_t end = cnt[h];
+    const uint32_t n = end - prev_end;
+    prev_end = end;
+    if (n == 0) continue;
+    const uint32_t* lam = slice + cnt[h] - n;  // (the cursor ends at the range's end)
+    float v = val[h];
+    if (n <= 8u) {  // the usual case: the match lengths in registers, read once
+      uint32_t lr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) lr[i] = (uint32_t)i < n ? lam[i] : 0u;
+      uint32_t top = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) top = max(top, lr[i]);
+      float pen = top >= allowed ? ts.dry_pen[top] : 0.0f;
+      for (uint32_t ml = top + 1; ml-- > allowed;) {
+        uint32_t act = 0;  // occurrences matching at this length
+#pragma unroll
+        for (int i = 0; i < 8; ++i) act += ((uint32_t)i < n && lr[i] >= ml) ? 1u : 0u;
+        const float pen_next = ml > allowed ? ts.dry_pen[ml - 1] : 0.0f;  // (read ahead)
+        uint32_t a = act;  // act subtractions of pen, four per loop step (:411)
+        for (; a >= 4u; a -= 4u) v = (((v - pen) - pen) - pen) - pen;
+        const float v2 = (v - pen) - pen;
+        v = (a & 2u) ? v2 : v;
+        const float v1 = v - pen;
+        v = (a & 1u) ? v1 : v;
+        pen = pen_next;
+      }
+    } else {  // an id with many matches: its lengths re-read per length
+      for (uint32_t ml = 33; ml-- > allowed;) {
+        uint32_t act = 0;
+        for (uint32_t i = 0; i < n; ++i) act += lam[i] >= ml ? 1u : 0u;
+        const float pen = ts.dry_pen[ml];
+        for (uint32_t a = 0; a < act; ++a) v = v - pen;  // :411
+      }
+    }
+    val[h] = v;
+  }
+  __syncthreads();
+  // the list: (id << 32 | value bits), sorted by id, built over the cursors
+  uint64_t* keys = (uint64_t*)cnt;  // [kDryMax]
+  if (tid == 0) ts.counter = 0;
+  __syncthreads();
+  for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+    const uint32_t id = hkey[h];
+    if (id != kEmptySlot) keys[atomicAdd(&ts.counter, 1u)] = ((uint64_t)id << 32) | __float_as_uint(val[h]);
+  }
+  __syncthreads();
+  const uint32_t nd = ts.counter;
+  bitonic_sort<true>(keys, nd);
+  for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = keys[i];
+  if (tid == 0) p.dry_count[row] = nd;
+  __syncthreads();
+}
+
 // DRY (sampler.rs:393-415) for one row, by its tail block. Over the last
 // dry_range history ids, for match lengths 32 down to allowed_length, every
 // earlier position whose n-gram equals the slice's suffix penalises the id
@@ -1746,14 +1896,19 @@ __device__ __forceinline__ float pre_stages_of(const Params& p, const RowXf& r, 
 // longer one is read where it lies and counted in the row's global hash
 // (2 * dry_cap slots) when the workspace has one, else in the LDS hash.
 // Returns false (the row cannot be run) when the penalised ids outnumber what
-// the hash or the list holds. Uses the first 32 KB of `lds`.
+// the hash or the list holds. Uses the first 32 KB of `lds`; after a slice of
+// up to kDryMax ids, the LDS hash (ids and values) is left for dry_lookup.
 template <int DT>
 __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32_t row, uint32_t* lds,
                                          const LibmTables& tab, TailShared& ts) {
   const uint32_t tid = threadIdx.x;
   const uint32_t L = min(r.hlen, r.dry_range);  // :394-396
+  if (L <= (uint32_t)kDryMax) {
+    dry_pass_lds<DT>(p, r, row, L, lds, tab, ts, p.dry_list + (size_t)row * p.dry_cap);
+    return true;  // (at most L <= kDryHash / 2 distinct ids)
+  }
   const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
-  const bool in_lds = L <= (uint32_t)kDryMax;
+  const bool in_lds = false;
   const bool global = !in_lds && p.dry_ghash;
   const uint32_t slots = global ? 2u * p.dry_cap : (uint32_t)kDryHash;  // a power of two
   const uint32_t shift = 32u - (31u - __builtin_clz(slots));
@@ -1832,7 +1987,8 @@ __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32
     for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = ~dl[i];
     wide_sort(dl, nd, (uint64_t*)lds);
     for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = ~dl[i];
-  } else {  // (id << 32 | value bits) from the LDS table into registers, then over the start of `lds`
+  } else {  // (id << 32 | value bits) from the LDS table into registers, then into LDS: over the
+            // cleared counters (at most kDryMax ids: the table stays for dry_lookup), or over the start
     constexpr int kPerT = kDryHash / kThreads;
     uint64_t mine[kPerT];
     uint32_t held = 0;  // bit q: slot tid + q * kThreads holds an id
@@ -1844,7 +2000,7 @@ __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32
       if (id != kEmptySlot) held |= 1u << q;
     }
     __syncthreads();
-    uint64_t* keys = (uint64_t*)lds;  // [kDryHash]
+    uint64_t* keys = in_lds ? (uint64_t*)cnt : (uint64_t*)lds;  // [kDryMax] or [kDryHash]
 #pragma unroll
     for (int q = 0; q < kPerT; ++q)
       if ((held >> q) & 1u) keys[atomicAdd(&ts.counter, 1u)] = mine[q];
@@ -1856,6 +2012,19 @@ __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32
   if (tid == 0) p.dry_count[row] = nd;
   __syncthreads();
   return true;
+}
+
+// The LDS DRY hash dry_pass leaves after a slice of up to kDryMax ids: the
+// slot holding `id`, or kDryHash when the row's DRY pass did not penalise it.
+__device__ __forceinline__ uint32_t dry_lookup(const uint32_t* hkey, uint32_t id) {
+  uint32_t h = (id * 0x9e3779b1u) >> 21;
+  for (int probe = 0; probe < kDryHash; ++probe) {
+    const uint32_t k = hkey[h];
+    if (k == id) return h;
+    if (k == kEmptySlot) break;
+    h = (h + 1) & (kDryHash - 1);
+  }
+  return kDryHash;
 }
 
 // ---------------------------------------------------------------- tail kernel
@@ -1966,6 +2135,45 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
     write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // more penalised ids than the DRY hash holds
     return;
   }
+  // A DRY row stays on the candidate path when DRY can only lower a value on
+  // its way to the key (penalties >= 0: dry_base >= 0; the stages after DRY
+  // and the temperature are non-decreasing, as the repetition penalty runs
+  // only for repeat_penalty > 0) and its slice fit the LDS hash: a penalised
+  // id outside the stream's candidates was below its wavefront's threshold
+  // before DRY and stays below it, and a penalised candidate gets its key
+  // recomputed here from its DRY value and its count in the repeat window
+  // (sampler.rs:203-245).
+  const bool dry_cand = r.dry && min(r.hlen, r.dry_range) <= (uint32_t)kDryMax && r.dry_base >= 0.0f;
+  if (dry_cand) {
+    const uint32_t* hkey = (const uint32_t*)s_keys + kDryKey;
+    const float* dval = (const float*)s_keys + kDryVal;
+    uint32_t* wcnt = (uint32_t*)s_keys + kDryCnt;  // over the sorted list, now in the row's DRY list
+    for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) wcnt[h] = 0;
+    __syncthreads();
+    if (r.use_hist) {
+      const uint32_t* win = p.history + (size_t)row * p.history_ld + r.wstart;
+      for (uint32_t j = tid; j < r.wn; j += kThreads) {
+        const uint32_t h = dry_lookup(hkey, win[j]);
+        if (h < (uint32_t)kDryHash) atomicAdd(&wcnt[h], 1u);
+      }
+    }
+    __syncthreads();
+    const float inv_t = r.do_temp ? r.inv_temp : 1.0f;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const uint32_t slot = 2u * (tid + (q / 2) * kThreads) + (q & 1);
+      if (!(slot < span && (slot & (cap_w - 1u)) < lc[q / 2] && lk[q] != 0ull)) continue;
+      const uint32_t id = ~(uint32_t)lk[q];
+      const uint32_t h = dry_lookup(hkey, id);
+      if (h < (uint32_t)kDryHash) lk[q] = comp_key(cand_key(special_post(r, dval[h], wcnt[h]) * inv_t), id);
+    }
+    if (p.logits_out)  // the stream kernel wrote these ids without DRY
+      for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
+        const uint32_t id = hkey[h];
+        if (id != kEmptySlot)
+          p.logits_out[(size_t)row * p.logits_out_ld + id] = special_post(r, dval[h], wcnt[h]) * inv_t;
+      }
+  }
 
   // 2. the largest wavefront threshold and the largest key, from the
   // wavefront records, reduced by every wavefront on its own (a record of all
@@ -1990,20 +2198,34 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
     km_l = max(km_l, (uint32_t)wr[q]);
   }
   const uint32_t th_w = wave_reduce32(th_l, MaxOp{});
-  const bool exact = th_w == 0xffffffffu || r.dry;
+  const bool exact = th_w == 0xffffffffu || (r.dry && !dry_cand);
   const uint64_t theta_max = exact ? ~0ull : (uint64_t)th_w << 32;
-  const uint64_t kmax = (uint64_t)wave_reduce32(km_l, MaxOp{}) << 32;
+  uint64_t kmax = (uint64_t)wave_reduce32(km_l, MaxOp{}) << 32;
   const bool all_kept = th_w == kMinValidOrd;  // (the same in every wavefront)
   uint64_t kmin = 0;
   if (all_kept) {
     const uint64_t d = wave_min_u64(kmn);
     if (lane == 0) ts.a_kmin[wave] = d;
   }
+  if (dry_cand) {  // the records' largest key predates DRY: the largest of the keys themselves
+    uint32_t km = 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      if ((valid >> q) & 1u) km = max(km, (uint32_t)(lk[q] >> 32));
+    const uint32_t d = wave_reduce32(km, MaxOp{});
+    if (lane == 0) ts.a_kmax[wave] = d;
+  }
   __syncthreads();  // every bucket count zeroed before any wavefront counts, and a_kmin complete
   if (all_kept) {
     kmin = ts.a_kmin[0];
 #pragma unroll
     for (int w = 1; w < kWavesPerBlock; ++w) kmin = ts.a_kmin[w] < kmin ? ts.a_kmin[w] : kmin;
+  }
+  if (dry_cand) {
+    uint32_t km = ts.a_kmax[0];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) km = max(km, ts.a_kmax[w]);
+    kmax = (uint64_t)km << 32;
   }
   // 3. kept keys: at or above every wavefront threshold (when every
   // wavefront kept all, every valid key)

@@ -140,6 +140,26 @@ def config2(batch: int = 64, vocab: int = 128256, seed: int = SEED_BASE + 2) -> 
                     xorshift_uniforms(batch, seed))
 
 
+def config2_dry(batch: int = 64, vocab: int = 128256, seed: int = SEED_BASE + 22) -> Workload:
+    """Config 2 with DRY on every row (multiplier 0.8, base 1.75, allowed length 2, range 1024) over
+    histories that end in a repeated motif of high-logit ids, so that DRY penalises candidates."""
+    w = config2(batch, vocab, seed)
+    rng = np.random.default_rng(seed + 1)
+    x = w.logits
+    H = int(w.history_len[0])
+    for b in range(batch):
+        top = np.argsort(-x[b])[:32].astype(np.uint32)
+        motif = rng.choice(top, 6, replace=False)
+        w.history[b, H - 48:H] = np.tile(motif, 8)
+        w.history[b, rng.integers(0, H - 100, 6)] = motif[0]
+    cfg = disabled_config(frequency_penalty=0.3, presence_penalty=0.2, repeat_penalty=1.05, repeat_last_n=512,
+                          temperature=0.7, top_k=50, top_p=0.9, min_p=0.05, dry_multiplier=0.8, dry_base=1.75,
+                          dry_allowed_length=2, dry_range=1024)
+    w.configs = [cfg] * batch
+    w.name = "config2_dry"
+    return w
+
+
 def config3(batch: int = 128, vocab: int = 128256, seed: int = SEED_BASE + 3) -> Workload:
     rng = np.random.default_rng(seed)
     logits = zipf_prior_logits(rng, batch, vocab, 3.0)

@@ -105,6 +105,24 @@ def test_baseline_configs_take_the_candidate_path(torch_gpu, cfg):
     assert counts["buckets"] + counts["sort"] == w.batch, counts
 
 
+def test_dry_rows_take_the_candidate_path(torch_gpu):
+    # config 2 with DRY on every row over histories ending in a repeated motif of high-logit ids:
+    # DRY lowers some candidates, and every row still finds its top M among the stream's candidates
+    from harness import gpu_sampler
+    w = wl.config2_dry()
+    banner(f"config2_dry B={w.batch} V={w.vocab}: parity and top-M paths")
+    s = gpu_sampler(w.batch, w.vocab)
+    s.count_paths(True)
+    try:
+        g = run_gpu(w, torch_gpu, logits_out=True)
+        counts = s.path_counts()
+    finally:
+        s.count_paths(False)
+    print(f"config2_dry paths: {counts}", flush=True)
+    compare(g, run_oracle(w, logits_out=True, n_threads=oracle_threads()), RTOL_F32, "config2_dry")
+    assert counts["exact"] == 0 and counts["buckets"] + counts["sort"] == w.batch, counts
+
+
 def mixed_workload(B, V, seed):
     """B rows cycling through every chain shape the config API offers, with ragged histories,
     empty (all -inf) rows and a row whose history is already full."""
