@@ -554,7 +554,8 @@ def bench_configs(args, torch):
 
     d = torch.device("cuda")
     lines = {}
-    for cfg_id in (1, 2, 3, 4, 5, "2dry"):
+    ids = [c if c == "2dry" else int(c) for c in args.config_ids.split(",")]
+    for cfg_id in ids:
         w = wl.config2_dry() if cfg_id == "2dry" else wl.BUILDERS[cfg_id]()
         name = w.name
         cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
@@ -617,7 +618,7 @@ def bench_configs(args, torch):
         torch.cuda.empty_cache()
     result = {
         "metric": "oxs_sample_batch per BASELINE config (config 5: one of its 8 steps)",
-        "value": lines["config2"]["rows_per_s"],
+        "value": lines["config2"]["rows_per_s"] if "config2" in lines else None,
         "unit": "rows/s",
         "higher_is_better": True,
         "n_gpus": 1,
@@ -733,6 +734,8 @@ def main():
     ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
     ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head", "configs"), default="sample",
                     help="sample: the headline config-2 line; decode / dfa_mask / lm_head / configs: secondary lines")
+    ap.add_argument("--config-ids", default="1,2,3,4,5,2dry",
+                    help="--workload configs: which configs (1-5, 2dry = config 2 with DRY on every row)")
     ap.add_argument("--lm-batch", type=int, default=64,
                     help="lm_head: q8_1 columns (64 = config 2's decode batch; 1 = the last prompt token)")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
