@@ -480,6 +480,62 @@ def bench_lm_head(args, torch):
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 
 
+def bench_read_floor(args, torch):
+    """The read floor of the stream phase on config 2: oxs_read_floor (the
+    stream kernel's grid and 16-byte non-temporal loads over the same
+    [64, 128256] f32 logits, nothing else) graph-replayed over the headline's
+    pool of distinct batches, timed with HIP events on the launch stream."""
+    import ctypes  # noqa: PLC0415
+    from oxide_sampler import _abi  # noqa: PLC0415
+    from oxide_sampler import workloads as wl  # noqa: PLC0415
+    lib = _abi.load_library()
+    w = wl.config2()
+    B, V = w.batch, w.vocab
+    P = pool_batches(B * V * 4)
+    pool = make_pool(torch, w, P)
+    d = torch.device("cuda")
+    sink = torch.empty(B * ((V + 8191) // 8192), dtype=torch.int32, device=d)
+    stream = torch.cuda.Stream()
+
+    def call(i):
+        _abi.check(lib.oxs_read_floor(ctypes.c_void_p(pool[i].data_ptr()), V, V, B, ctypes.c_void_p(sink.data_ptr()),
+                                      ctypes.c_void_p(stream.cuda_stream)), "oxs_read_floor")
+
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(P):
+            call(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(P):
+            call(i)
+    reps = max(3, args.steps // P)
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup // P)):
+            graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * P)
+    nbytes = B * V * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    result = {
+        "metric": "read floor of the stream phase: one pass over config 2's logits",
+        "value": gbs, "unit": "GB/s", "higher_is_better": True, "n_gpus": 1, "steps": reps * P,
+        "us_per_launch": us, "bytes_per_launch": nbytes, "frac_of_peak": gbs / HBM_PEAK_GBS,
+        "dtype": "f32", "data": f"synthetic: the headline's pool of {P} distinct config-2 batches",
+        "config": {"workload": "read_floor: oxs_read_floor over [64, 128256] f32, the stream kernel's grid "
+                               "(1024 blocks of 8192 logits, eight 16-byte non-temporal loads per thread)"},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def pool_batches(batch_bytes, at_least=2):
     """Distinct input batches whose total exceeds twice the Infinity Cache, so
     a rotation over them streams from HBM."""
@@ -732,7 +788,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only 8 plain 256 MiB device copies (scale for the rocprofv3 byte counters)")
     ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
-    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head", "configs"), default="sample",
+    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head", "configs", "read_floor"),
+                    default="sample",
                     help="sample: the headline config-2 line; decode / dfa_mask / lm_head / configs: secondary lines")
     ap.add_argument("--config-ids", default="1,2,3,4,5,2dry",
                     help="--workload configs: which configs (1-5, 2dry = config 2 with DRY on every row)")
@@ -778,6 +835,8 @@ def main():
     if args.workload == "lm_head":
         bench_lm_head(args, torch)
         return
+    if args.workload == "read_floor":
+        return bench_read_floor(args, torch)
     if args.workload == "configs":
         bench_configs(args, torch)
         return

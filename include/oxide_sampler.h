@@ -229,6 +229,17 @@ int oxs_sampler_count_paths(oxs_sampler* sampler, int enable);
 int oxs_sampler_path_counts(const oxs_sampler* sampler, uint32_t counts[4]);
 
 /*
+ * Diagnostics: the read floor of the sampler's stream phase. Reads `batch`
+ * rows of `vocab` f32 logits (16-byte aligned, vocab and logits_ld multiples
+ * of 4) in the stream kernel's grid and load pattern and nothing else; each
+ * (row, 8192-logit chunk) block writes one word to sink (batch * ceil(vocab /
+ * 8192) words). No counterpart in the reference: it measures how fast one
+ * pass over the logits can go.
+ */
+int oxs_read_floor(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t batch, uint32_t* sink,
+                   void* stream);
+
+/*
  * Samples every row of `batch` on `stream` (a hipStream_t; NULL = default
  * stream). Replaces B serial calls of
  *   AcademicSamplerEngine::sample_token(&self, logits: &mut [f32],

@@ -2422,6 +2422,34 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const Params p) {
   wave_chain<DT>(p, c, row, meff, bf, rs, s_tab);
 }
 
+// ---------------------------------------------------------------- read floor
+
+// The stream kernel's access pattern with nothing else: one block per
+// (row, 8192-float chunk), eight 16-byte non-temporal loads per thread, the
+// chunk's largest value (bits) written to sink[block]. Its time per launch is
+// the floor one pass over the logits can reach.
+__global__ __launch_bounds__(kThreads) void read_floor_kernel(const float* __restrict__ x, int64_t ld, uint32_t V,
+                                                              uint32_t S, uint32_t* __restrict__ sink) {
+  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x - row * S;
+  const uint32_t c0 = chunk * (uint32_t)kMaxChunk, c1 = min(c0 + (uint32_t)kMaxChunk, V);
+  const char* rp = (const char*)(x + (size_t)row * ld);
+  u32x4 q[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const uint32_t base = c0 + s * kThreads * 4 + threadIdx.x * 4;
+    const uint32_t at = base < c1 ? base : V - 4;
+    q[s] = __builtin_nontemporal_load((const u32x4*)(rp + (size_t)at * 4));
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) m = max(max(max(m, q[s].x), max(q[s].y, q[s].z)), q[s].w);
+  m = wave_reduce32(m, MaxOp{});
+  __shared__ uint32_t sm[kWavesPerBlock];
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = max(max(sm[0], sm[1]), max(sm[2], sm[3]));
+}
+
 // ---------------------------------------------------------------- argmax
 
 // launch_cuda_argmax (oxide-backend-cuda/src/kernels/sampling_dfa.cu:2-68,
@@ -3040,6 +3068,18 @@ int oxs_argmax(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t 
   if (!logits || !out_token || logits_ld < (int64_t)vocab) return OXS_ERR_INVALID_ARGUMENT;
   hipLaunchKernelGGL(oxs::argmax_kernel, dim3(batch), dim3(oxs::kArgmaxThreads), 0, (hipStream_t)stream, logits,
                      vocab, logits_ld, out_token, out_max_val);
+  return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+}
+
+int oxs_read_floor(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t batch, uint32_t* sink,
+                   void* stream) {
+  if (batch == 0) return OXS_OK;
+  if (!logits || !sink || vocab < 4 || vocab % 4 != 0 || logits_ld < (int64_t)vocab || logits_ld % 4 != 0 ||
+      ((uintptr_t)logits & 15u) != 0)
+    return OXS_ERR_INVALID_ARGUMENT;
+  const uint32_t S = (vocab + oxs::kMaxChunk - 1) / oxs::kMaxChunk;
+  hipLaunchKernelGGL(oxs::read_floor_kernel, dim3(batch * S), dim3(oxs::kThreads), 0, (hipStream_t)stream, logits,
+                     logits_ld, vocab, S, sink);
   return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
 }
 

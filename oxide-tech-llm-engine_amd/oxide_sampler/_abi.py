@@ -59,6 +59,7 @@ EXPORTED_SYMBOLS = (
     "oxs_sampler_workspace_bytes",
     "oxs_sampler_count_paths",
     "oxs_sampler_path_counts",
+    "oxs_read_floor",
     "oxs_sample_batch",
     "oxs_sample_batch_static",
     "oxs_decode_step",
@@ -226,6 +227,9 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.oxs_sampler_path_counts.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]
     lib.oxs_sample_batch.restype = ctypes.c_int
     lib.oxs_sample_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(OxsBatch), ctypes.c_void_p]
+    lib.oxs_read_floor.restype = ctypes.c_int
+    lib.oxs_read_floor.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int64, ctypes.c_uint32,
+                                   ctypes.c_void_p, ctypes.c_void_p]
     lib.oxs_sample_batch_static.restype = ctypes.c_int
     lib.oxs_sample_batch_static.argtypes = [ctypes.POINTER(OxsBatch), ctypes.c_void_p]
     lib.oxs_decode_step.restype = ctypes.c_int
