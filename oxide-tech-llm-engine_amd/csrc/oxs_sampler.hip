@@ -2456,53 +2456,70 @@ __global__ __launch_bounds__(kThreads) void read_floor_kernel(const float* __res
 // :161-178): per row, the largest logit above -1e30 (its running maximum
 // starts at -1e30 and only a strictly larger value replaces it, so NaN and
 // values <= -1e30 are never taken); a row without one gives token 0 and value
-// -1e30. Among equal maxima the lower token id wins. One 1024-thread block
-// per row, eight 16-byte loads in flight per thread when the row allows them.
+// -1e30. Among equal maxima the lower token id wins, and -0.0 equals +0.0, so
+// the value returned is the winning logit's own bits (as the sequential scan
+// returns them). One 1024-thread block per row, eight non-temporal 16-byte
+// loads in flight per thread when the row allows them; each lane keeps the
+// (value, id) of its first largest logit, its ids visited in increasing order.
 constexpr int kArgmaxThreads = 1024;
+struct ArgBest {
+  float v;
+  uint32_t i;  // 0xffffffff: nothing above the floor yet
+};
+__device__ __forceinline__ void arg_take(ArgBest& b, float v, uint32_t i) {
+  const bool t = v > b.v;  // strict: an equal value at a higher id never replaces
+  b.v = t ? v : b.v;
+  b.i = t ? i : b.i;
+}
+__device__ __forceinline__ void arg_merge(ArgBest& b, float ov, uint32_t oi) {
+  const bool t = ov > b.v || (ov == b.v && oi < b.i);
+  b.v = t ? ov : b.v;
+  b.i = t ? oi : b.i;
+}
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, uint32_t V,
                                                                int64_t ld, uint32_t* __restrict__ out_token,
                                                                float* __restrict__ out_val) {
-  __shared__ uint64_t s_best[kArgmaxThreads / 64];
+  __shared__ float s_v[kArgmaxThreads / 64];
+  __shared__ uint32_t s_i[kArgmaxThreads / 64];
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   const float* x = logits + (size_t)row * (size_t)ld;
   const float floor_v = -1e30f;
-  uint64_t best = 0;  // (order key << 32 | ~id), 0 = nothing above the floor
-  auto take = [&](float v, uint32_t i) {
-    if (v > floor_v) {
-      const uint64_t k = ((uint64_t)f2ord(v) << 32) | (uint64_t)(~i);
-      best = k > best ? k : best;
-    }
-  };
+  ArgBest b{floor_v, 0xffffffffu};
   const bool vec = ((uintptr_t)x % 16 == 0);
   const uint32_t nv = vec ? V / 4 : 0;
   constexpr int kUnroll = 8;  // 16-byte loads in flight per thread
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
   for (uint32_t q0 = tid; q0 < nv; q0 += kArgmaxThreads * kUnroll) {
-    float4 f[kUnroll];
+    f32x4v f[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint32_t q = q0 + u * kArgmaxThreads;
-      f[u] = *(const float4*)(x + 4 * (size_t)(q < nv ? q : q0));  // repeats of q0 change no maximum
+      f[u] = __builtin_nontemporal_load((const f32x4v*)(x + 4 * (size_t)(q < nv ? q : q0)));  // in bounds
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint32_t q = q0 + u * kArgmaxThreads;
       if (q < nv) {
-        take(f[u].x, 4 * q);
-        take(f[u].y, 4 * q + 1);
-        take(f[u].z, 4 * q + 2);
-        take(f[u].w, 4 * q + 3);
+        arg_take(b, f[u].x, 4 * q);
+        arg_take(b, f[u].y, 4 * q + 1);
+        arg_take(b, f[u].z, 4 * q + 2);
+        arg_take(b, f[u].w, 4 * q + 3);
       }
     }
   }
-  for (uint32_t i = 4 * nv + tid; i < V; i += kArgmaxThreads) take(x[i], i);
-  best = wave_max_u64(best);
-  if ((tid & 63) == 0) s_best[tid >> 6] = best;
+  for (uint32_t i = 4 * nv + tid; i < V; i += kArgmaxThreads) arg_take(b, x[i], i);  // higher ids than above
+  for (int o = 32; o >= 1; o >>= 1) arg_merge(b, __shfl_xor(b.v, o), (uint32_t)__shfl_xor((int)b.i, o));
+  if ((tid & 63) == 0) {
+    s_v[tid >> 6] = b.v;
+    s_i[tid >> 6] = b.i;
+  }
   __syncthreads();
   if (tid == 0) {
-    uint64_t b = s_best[0];
-    for (int w = 1; w < kArgmaxThreads / 64; ++w) b = s_best[w] > b ? s_best[w] : b;
-    if (out_token) out_token[row] = b ? ~(uint32_t)b : 0u;
-    if (out_val) out_val[row] = b ? ord2f((uint32_t)(b >> 32)) : floor_v;
+    ArgBest r{s_v[0], s_i[0]};
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) arg_merge(r, s_v[w], s_i[w]);
+    const bool none = r.i == 0xffffffffu;
+    if (out_token) out_token[row] = none ? 0u : r.i;
+    if (out_val) out_val[row] = none ? floor_v : r.v;
   }
 }
 

@@ -424,6 +424,11 @@ def test_oracle_argmax_floor_cases():
     x = rng.standard_normal(5000).astype(np.float32)
     x[[10, 4000]] = 7.0
     assert oracle.argmax_floor_host(x) == (10, 7.0)
+    # -0.0 equals +0.0: the first of them wins and keeps its own sign bit
+    tok, val = oracle.argmax_floor_host(np.array([-1.0, -0.0, 0.0, -3.0], np.float32))
+    assert tok == 1 and np.float32(val).view(np.uint32) == 0x80000000
+    tok, val = oracle.argmax_floor_host(np.array([-1.0, 0.0, -0.0], np.float32))
+    assert tok == 1 and np.float32(val).view(np.uint32) == 0
 
 
 @pytest.mark.gpu
@@ -438,6 +443,10 @@ def test_gpu_argmax_matches_oracle(torch_gpu, B, V, ld):
         x[1, :] = -np.inf
         x[2, : V // 2] = np.nan
         x[2, V // 2:] = np.float32(-2e30)
+    if B > 3:  # the maximum is zero, -0.0 first: its bits come back
+        x[3, :] = np.float32(-1.0)
+        x[3, V // 5] = np.float32(-0.0)
+        x[3, V // 2] = np.float32(0.0)
     print(f"\n[case] argmax B={B} V={V} ld={ld}", flush=True)
     d = t.from_numpy(x).to("cuda")
     tok = t.zeros(B, dtype=t.int32, device="cuda")
@@ -446,6 +455,7 @@ def test_gpu_argmax_matches_oracle(torch_gpu, B, V, ld):
     _abi.check(lib.oxs_argmax(ctypes.c_void_p(d.data_ptr()), V, ld, B, ctypes.c_void_p(tok.data_ptr()),
                               ctypes.c_void_p(val.data_ptr()), None), "oxs_argmax")
     t.cuda.synchronize()
+    got_bits = val.cpu().numpy().view(np.uint32)
     for b in range(B):
         want = oracle.argmax_floor_host(x[b, :V])
-        assert int(tok[b]) == want[0] and float(val[b]) == np.float32(want[1]), (b, int(tok[b]), want)
+        assert int(tok[b]) == want[0] and got_bits[b] == np.float32(want[1]).view(np.uint32), (b, int(tok[b]), want)
