@@ -622,9 +622,21 @@ __device__ __forceinline__ void process_unit(const Params& p, uint32_t row, uint
     // unemitted values are < theta_f, so their scaled values are <= theta_f * inv_t
     th_ord = inv_t == 1.0f ? theta : f2ord(theta_f * inv_t) + 1u;
   }
-  uint32_t smask = 0;  // bit i: v[i] >= theta_f (false for -inf and NaN)
+  uint32_t smask = 0;  // bit i: v[i] >= theta_f (false for -inf; a NaN's bit is dropped at emission)
+  if (theta_f < __builtin_inff()) {
+    // bit i is the sign of v[i] - tq, inverted: for a finite or -FLT_MAX
+    // threshold tq (-0.0 in place of +0.0, so that -0.0 - tq is +0.0) the
+    // difference is >= +0.0 exactly when v[i] >= theta_f. v_alignbit shifts
+    // each sign bit in, value NE-1 first, so value i lands on bit i.
+    const float tq = theta_f == 0.0f ? -0.0f : theta_f;
+    uint32_t below = 0;
 #pragma unroll
-  for (int i = 0; i < NE; ++i) smask |= (v[i] >= theta_f ? 1u : 0u) << i;
+    for (int i = NE - 1; i >= 0; --i) below = __builtin_amdgcn_alignbit(below, __float_as_uint(v[i] - tq), 31);
+    smask = ~below & (NE == 32 ? 0xffffffffu : ((1u << (NE & 31)) - 1u));
+  } else {  // an infinite or NaN threshold
+#pragma unroll
+    for (int i = 0; i < NE; ++i) smask |= (v[i] >= theta_f ? 1u : 0u) << i;
+  }
 
   // ---- survivors into this wavefront's list; slots from the wavefront's
   // ballot of the lanes that emit, in lane order

@@ -218,6 +218,42 @@ def wide_workload(B, V, seed, dtype="f32"):
                        mu=np.full(B, 18.0, np.float32))
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_signed_zero_threshold(torch_gpu, dtype):
+    # rows of negative logits with one +0.0 or -0.0 every 80 ids: each stream wavefront's
+    # threshold is exactly zero, and -0.0 must count as >= it (a -0.0 of lower id ranks
+    # before a later +0.0 among the tied top 50)
+    B, V = 16, 128256
+    rng = np.random.default_rng(77)
+    x = (-1.0 - 4.0 * rng.random((B, V))).astype(np.float32)
+    for b in range(B):
+        at = np.arange(b % 80, V, 80)
+        x[b, at] = np.where(rng.random(at.size) < 0.5, np.float32(-0.0), np.float32(0.0))
+    logits = wl.f32_to_bf16_bits(x) if dtype == "bf16" else x
+    # (temperature 1: at another temperature a key equal to a wavefront's threshold lies below the
+    # scaled bound that proves the top M, and those rows take the exact re-scan by design)
+    configs = [wl.disabled_config(top_k=50, top_p=0.95) if b % 2 else
+               wl.disabled_config(top_k=200, min_p=0.01, repeat_penalty=1.2, repeat_last_n=64)
+               for b in range(B)]
+    history = rng.integers(0, V, size=(B, 64), dtype=np.uint32)
+    w = wl.Workload(name=f"signed zeros {dtype}", logits=logits, dtype=dtype, configs=configs, history=history,
+                    history_len=np.full(B, 64, np.uint32), uniforms=wl.xorshift_uniforms(B, 78))
+    banner(f"signed-zero thresholds B={B} V={V} {dtype}")
+    from harness import gpu_sampler
+    s = gpu_sampler(w.batch, w.vocab)
+    s.count_paths(True)
+    try:
+        g = run_gpu(w, torch_gpu, kept_ld=512, logits_out=True)
+        counts = s.path_counts()
+    finally:
+        s.count_paths(False)
+    compare(g, run_oracle(w, kept_ld=512, logits_out=True), RTOL_BF16 if dtype == "bf16" else RTOL_F32,
+            f"signed zeros {dtype}")
+    # about 26 zeros per wavefront fit its 32-key list: every row is proven from the candidates
+    # (so a dropped -0.0 key would show as a wrong kept set, not hide behind the exact re-scan)
+    assert counts["exact"] == 0 and counts["buckets"] + counts["sort"] == B, counts
+
+
 @pytest.mark.parametrize("V,dtype", [(60000, "f32"), (151936, "bf16"), (1500, "f32")])
 def test_wide_top_k(torch_gpu, V, dtype):
     # top_k 1025, 2000 and 50000 (kept to V when larger) beside ordinary rows: the wide kernel's
