@@ -323,7 +323,8 @@ int oxs_decode_step(oxs_sampler* sampler, const oxs_batch* batch, const oxs_deco
  * reference's running maximum starts at -1e30 and only a strictly larger value
  * replaces it); a row without one gives token 0 and -1e30. Among equal maxima
  * the lower token id wins (the reference's order depends on its thread
- * layout). out_max_val may be NULL. Asynchronous; allocates nothing.
+ * layout); -0.0 and +0.0 are equal, and out_max_val receives the winning
+ * logit's own bits. out_max_val may be NULL. Asynchronous; allocates nothing.
  * OXS_ERR_SHAPE_MISMATCH for vocab 0.
  */
 int oxs_argmax(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t batch, uint32_t* out_token,
