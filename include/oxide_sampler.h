@@ -322,10 +322,17 @@ int oxs_decode_step(oxs_sampler* sampler, const oxs_batch* batch, const oxs_deco
  * value above -1e30 and its token id, NaN and values <= -1e30 never taken (the
  * reference's running maximum starts at -1e30 and only a strictly larger value
  * replaces it); a row without one gives token 0 and -1e30. Among equal maxima
- * the lower token id wins (the reference's order depends on its thread
- * layout); -0.0 and +0.0 are equal, and out_max_val receives the winning
- * logit's own bits. out_max_val may be NULL. Asynchronous; allocates nothing.
- * OXS_ERR_SHAPE_MISMATCH for vocab 0.
+ * the winner is the reference's, which follows its thread layout (not the
+ * lowest id): with batch > 1 (one 1024-thread block per row, :2-68) the id
+ * whose thread t = id % 1024 has the smallest bit-reversed 5-bit warp index
+ * (t / 32), then lane index (t % 32), and that thread's first such id; with
+ * batch 1 (24 blocks of 256 threads striding by 6144, :70-159) the same over
+ * block, warp and lane of id % 6144. -0.0 and +0.0 are equal, and out_max_val
+ * receives the winning logit's own bits. out_max_val may be NULL.
+ * Asynchronous; allocates nothing. Rows are split over several blocks, which
+ * meet in file-scope device slots (as the reference's batch-1 path does):
+ * calls that overlap on one device race on them. OXS_ERR_SHAPE_MISMATCH for
+ * vocab 0; OXS_ERR_INVALID_ARGUMENT for vocab > 2^30.
  */
 int oxs_argmax(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t batch, uint32_t* out_token,
                float* out_max_val, void* stream);

@@ -561,19 +561,74 @@ void oxo_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, u
   }
 }
 
-// launch_cuda_argmax (sampling_dfa.cu:2-68): the running maximum starts at
-// -1e30 and only a strictly larger value replaces it; the lower id wins ties.
-void oxo_argmax_floor(const float* row, uint32_t vocab, uint32_t* token, float* value) {
-  float best = -1e30f;
-  uint32_t idx = 0;
-  for (uint32_t i = 0; i < vocab; ++i) {
-    if (row[i] > best) {
-      best = row[i];
-      idx = i;
+// launch_cuda_argmax (sampling_dfa.cu:161-178), simulated thread by thread.
+// Which of several equal maxima wins depends on the kernels' thread layout,
+// so the oracle runs that layout literally:
+//  - each thread scans ids start, start + stride, ... with a running maximum
+//    that starts at (-1e30, id 0) and is replaced only by a strictly larger
+//    value (:13-23, :81-91);
+//  - a warp of 32 lanes reduces with __shfl_down_sync at offsets 16, 8, 4, 2,
+//    1: lane l takes lane l + off's pair only when that value is strictly
+//    larger; a source lane past 31 is the lane itself (:26-33);
+//  - lane 0 of each warp stores its pair, and the first warp reduces the
+//    stored pairs the same way, lanes past the warp count holding
+//    (-1e30, 0) (:44-58).
+// batch > 1: one 1024-thread block per row (:2-68, :173-175).
+// batch == 1: 24 blocks of 256 threads stride the row by 6144, each block
+// reduces to one pair, and one warp reduces the 24 pairs (:70-159, :165-171).
+namespace {
+struct ArgPair {
+  float v;
+  uint32_t i;
+};
+ArgPair arg_thread_scan(const float* row, uint32_t vocab, uint32_t start, uint32_t stride) {
+  ArgPair p{-1e30f, 0u};
+  for (uint64_t i = start; i < vocab; i += stride)
+    if (row[i] > p.v) p = ArgPair{row[i], (uint32_t)i};
+  return p;
+}
+ArgPair arg_warp_tree(const ArgPair (&in)[32]) {
+  ArgPair lane[32];
+  for (int l = 0; l < 32; ++l) lane[l] = in[l];
+  for (int off = 16; off > 0; off >>= 1) {
+    ArgPair before[32];
+    for (int l = 0; l < 32; ++l) before[l] = lane[l];  // every lane reads before any lane updates
+    for (int l = 0; l < 32; ++l) {
+      const ArgPair other = l + off < 32 ? before[l + off] : before[l];
+      if (other.v > before[l].v) lane[l] = other;
     }
   }
-  *token = idx;
-  *value = best;
+  return lane[0];
+}
+// One block of `threads` threads (a multiple of 32) whose thread t scans from
+// first + t with the given stride.
+ArgPair arg_block(const float* row, uint32_t vocab, uint32_t threads, uint32_t first, uint32_t stride) {
+  ArgPair warps[32];
+  const uint32_t nw = threads / 32;
+  for (uint32_t w = 0; w < nw; ++w) {
+    ArgPair lanes[32];
+    for (uint32_t l = 0; l < 32; ++l) lanes[l] = arg_thread_scan(row, vocab, first + w * 32 + l, stride);
+    warps[w] = arg_warp_tree(lanes);
+  }
+  for (uint32_t w = nw; w < 32; ++w) warps[w] = ArgPair{-1e30f, 0u};
+  return arg_warp_tree(warps);
+}
+}  // namespace
+
+void oxo_argmax_floor(const float* row, uint32_t vocab, uint32_t batch, uint32_t* token, float* value) {
+  ArgPair r;
+  if (batch == 1) {
+    constexpr uint32_t kBlocks = 24, kThreadsPer = 256;
+    ArgPair blocks[32];
+    for (uint32_t b = 0; b < kBlocks; ++b)
+      blocks[b] = arg_block(row, vocab, kThreadsPer, b * kThreadsPer, kBlocks * kThreadsPer);
+    for (uint32_t b = kBlocks; b < 32; ++b) blocks[b] = ArgPair{-1e30f, 0u};
+    r = arg_warp_tree(blocks);
+  } else {
+    r = arg_block(row, vocab, 1024, 0, 1024);
+  }
+  *token = r.i;
+  *value = r.v;
 }
 
 // ---------------------------------------------------------------- LM head (Q8_0 x q8_1)

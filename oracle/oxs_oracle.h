@@ -99,8 +99,10 @@ void oxo_gbnf_mask(const uint32_t* ranges, uint32_t num_ranges, const uint32_t* 
                    uint32_t vocab, uint32_t* mask);
 void oxo_ascii_mask(const uint8_t* allowed_ascii, const uint16_t* token_ascii, uint32_t vocab, uint32_t* mask);
 
-/* oxs_argmax on one row (launch_cuda_argmax, sampling_dfa.cu:2-68). */
-void oxo_argmax_floor(const float* row, uint32_t vocab, uint32_t* token, float* value);
+/* oxs_argmax on one row of a launch over `batch` rows (launch_cuda_argmax,
+ * sampling_dfa.cu:161-178): batch 1 takes the 24-block path, any other batch
+ * the one-block-per-row path; each is simulated thread by thread. */
+void oxo_argmax_floor(const float* row, uint32_t vocab, uint32_t batch, uint32_t* token, float* value);
 
 /* glibc's expf etc., exported so tests can compare the device emulation. */
 float oxo_expf(float x);

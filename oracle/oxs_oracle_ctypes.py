@@ -53,7 +53,7 @@ def load() -> ctypes.CDLL:
     lib.oxo_decode_step.restype = ctypes.c_int
     lib.oxo_decode_step.argtypes = [vp, vp, ctypes.c_int]
     lib.oxo_argmax_floor.restype = None
-    lib.oxo_argmax_floor.argtypes = [vp, ctypes.c_uint32, vp, vp]
+    lib.oxo_argmax_floor.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, vp, vp]
     lib.oxo_raw_argmax.restype = ctypes.c_uint32
     lib.oxo_raw_argmax.argtypes = [vp, ctypes.c_uint32]
     lib.oxo_gbnf_mask.restype = None
@@ -243,12 +243,12 @@ def ascii_mask_host(allowed, token_ascii):
     return mask[: (vocab + 31) // 32]
 
 
-def argmax_floor_host(row):
-    """oxo_argmax_floor: (token, value) of one f32 row."""
+def argmax_floor_host(row, batch=2):
+    """oxo_argmax_floor: (token, value) of one f32 row of a launch over `batch` rows."""
     row = np.ascontiguousarray(row, dtype=np.float32)
     tok = np.zeros(1, np.uint32)
     val = np.zeros(1, np.float32)
-    load().oxo_argmax_floor(_ptr(row), row.shape[0], _ptr(tok), _ptr(val))
+    load().oxo_argmax_floor(_ptr(row), row.shape[0], batch, _ptr(tok), _ptr(val))
     return int(tok[0]), float(val[0])
 
 

@@ -2464,75 +2464,174 @@ __global__ __launch_bounds__(kThreads) void read_floor_kernel(const float* __res
 
 // ---------------------------------------------------------------- argmax
 
-// launch_cuda_argmax (oxide-backend-cuda/src/kernels/sampling_dfa.cu:2-68,
-// :161-178): per row, the largest logit above -1e30 (its running maximum
-// starts at -1e30 and only a strictly larger value replaces it, so NaN and
-// values <= -1e30 are never taken); a row without one gives token 0 and value
-// -1e30. Among equal maxima the lower token id wins, and -0.0 equals +0.0, so
-// the value returned is the winning logit's own bits (as the sequential scan
-// returns them). One 1024-thread block per row, eight non-temporal 16-byte
-// loads in flight per thread when the row allows them; each lane keeps the
-// (value, id) of its first largest logit, its ids visited in increasing order.
-constexpr int kArgmaxThreads = 1024;
-struct ArgBest {
-  float v;
-  uint32_t i;  // 0xffffffff: nothing above the floor yet
-};
-__device__ __forceinline__ void arg_take(ArgBest& b, float v, uint32_t i) {
-  const bool t = v > b.v;  // strict: an equal value at a higher id never replaces
-  b.v = t ? v : b.v;
-  b.i = t ? i : b.i;
+// launch_cuda_argmax (oxide-backend-cuda/src/kernels/sampling_dfa.cu:161-178):
+// per row, the largest logit above -1e30 (its running maxima start at -1e30
+// and only a strictly larger value replaces one, so NaN and values <= -1e30
+// are never taken); a row without one gives token 0 and value -1e30.
+//
+// Which of several equal maxima the reference returns follows from its thread
+// layout. With more than one row (one 1024-thread block per row, :2-68),
+// thread t keeps the first maximum among ids i = t (mod 1024), and the two
+// __shfl_down_sync trees (offsets 16 .. 1, the lower lane kept unless the
+// other value is strictly larger) keep, among tied lanes, the one whose 5-bit
+// index reversed bit for bit is smallest: first over the warps, then over the
+// lanes of the winning warp. With one row (24 blocks of 256 threads striding
+// the row by 6144, :70-159) the same holds for the block, then the warp (of
+// 8), then the lane. -0.0 equals +0.0 there, and the value returned is the
+// winning logit's own bits.
+//
+// Here every logit becomes a 64-bit key ordered exactly as that rule orders
+// candidates: (order-preserving value bits << 32) | (priority << 1) | (1 for
+// -0.0), the priority being the reversed warp and lane (and block) indices
+// and the thread's visiting order, complemented so that larger is preferred.
+// A total order reduces in any grouping, so a row is split over as many
+// blocks as fill the GPU; each block folds its best key into the row's slot
+// with a device-scope atomic maximum, and the row's last block (a ticket)
+// writes the result and clears the slot for the next launch. The slots are
+// file-scope device memory, as the reference's g_argmax_scratch_* are: calls
+// that overlap on one device race on them.
+constexpr uint32_t kArgRows = 16384;  // rows per launch (the host splits larger batches)
+static __device__ uint64_t g_arg_best[kArgRows];
+static __device__ uint32_t g_arg_ticket[kArgRows];
+
+__device__ __forceinline__ uint32_t rev5(uint32_t x) { return __builtin_bitreverse32(x) >> 27; }
+__device__ __forceinline__ uint32_t rev3(uint32_t x) { return __builtin_bitreverse32(x) >> 29; }
+
+// The priority of logit i (31 bits, larger preferred) and its inverse. ONE:
+// the batch-1 layout (q = i / 6144 < 2^18), else the 1024-thread layout
+// (q = i >> 10 < 2^21); both hold for i < 2^30.
+template <bool ONE>
+__device__ __forceinline__ uint32_t arg_priority(uint32_t i) {
+  if constexpr (ONE) {
+    const uint32_t q = i / 6144u, g = i - q * 6144u;
+    return ((31u - rev5(g >> 8)) << 26) | ((7u - rev3((g >> 5) & 7u)) << 23) | ((31u - rev5(g & 31u)) << 18) |
+           (0x3ffffu - q);
+  } else {
+    const uint32_t q = i >> 10, t = i & 1023u;
+    return ((31u - rev5(t >> 5)) << 26) | ((31u - rev5(t & 31u)) << 21) | (0x1fffffu - q);
+  }
 }
-__device__ __forceinline__ void arg_merge(ArgBest& b, float ov, uint32_t oi) {
-  const bool t = ov > b.v || (ov == b.v && oi < b.i);
-  b.v = t ? ov : b.v;
-  b.i = t ? oi : b.i;
+template <bool ONE>
+__device__ __forceinline__ uint32_t arg_index(uint32_t pr) {
+  if constexpr (ONE) {
+    const uint32_t blk = rev5(31u - (pr >> 26)), w = rev3(7u - ((pr >> 23) & 7u)), l = rev5(31u - ((pr >> 18) & 31u));
+    return (0x3ffffu - (pr & 0x3ffffu)) * 6144u + blk * 256u + w * 32u + l;
+  } else {
+    const uint32_t w = rev5(31u - (pr >> 26)), l = rev5(31u - ((pr >> 21) & 31u));
+    return (0x1fffffu - (pr & 0x1fffffu)) * 1024u + w * 32u + l;
+  }
 }
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, uint32_t V,
-                                                               int64_t ld, uint32_t* __restrict__ out_token,
-                                                               float* __restrict__ out_val) {
-  __shared__ float s_v[kArgmaxThreads / 64];
-  __shared__ uint32_t s_i[kArgmaxThreads / 64];
-  const uint32_t row = blockIdx.x, tid = threadIdx.x;
+template <bool ONE>
+__device__ __forceinline__ uint64_t arg_key(float v, uint32_t i) {
+  const uint32_t u = __float_as_uint(v);
+  const uint64_t k = ((uint64_t)f2ord(v) << 32) | (arg_priority<ONE>(i) << 1) | (u == 0x80000000u ? 1u : 0u);
+  return v > -1e30f ? k : 0ull;  // (false for NaN)
+}
+template <bool ONE>
+__device__ __forceinline__ void arg_write(uint64_t k, uint32_t row, uint32_t* out_token, float* out_val) {
+  uint32_t tok = 0;
+  float val = -1e30f;
+  if (k) {
+    const uint32_t o = (uint32_t)(k >> 32);
+    tok = arg_index<ONE>((uint32_t)k >> 1);
+    val = o == 0x80000000u ? ((k & 1u) ? -0.0f : 0.0f) : ord2f(o);
+  }
+  out_token[row] = tok;
+  if (out_val) out_val[row] = val;
+}
+
+// One block per (row, chunk of NS * 1024 logits); NS 16-byte loads per thread
+// in flight (VEC: 16-byte aligned rows, V % 4 == 0), or scalar loads.
+template <bool ONE, int NS, bool VEC>
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restrict__ logits, uint32_t V, int64_t ld,
+                                                          uint32_t S, uint32_t* __restrict__ out_token,
+                                                          float* __restrict__ out_val) {
+  constexpr uint32_t CH = NS * kThreads * 4;
+  __shared__ uint64_t s_best[kWavesPerBlock];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x - row * S;
+  const uint32_t c0 = chunk * CH;
   const float* x = logits + (size_t)row * (size_t)ld;
-  const float floor_v = -1e30f;
-  ArgBest b{floor_v, 0xffffffffu};
-  const bool vec = ((uintptr_t)x % 16 == 0);
-  const uint32_t nv = vec ? V / 4 : 0;
-  constexpr int kUnroll = 8;  // 16-byte loads in flight per thread
-  typedef float f32x4v __attribute__((ext_vector_type(4)));
-  for (uint32_t q0 = tid; q0 < nv; q0 += kArgmaxThreads * kUnroll) {
-    f32x4v f[kUnroll];
+  float f[NS][4];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t q = q0 + u * kArgmaxThreads;
-      f[u] = __builtin_nontemporal_load((const f32x4v*)(x + 4 * (size_t)(q < nv ? q : q0)));  // in bounds
-    }
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t base = c0 + s * kThreads * 4 + tid * 4;
+    if constexpr (VEC) {
+      const uint32_t at = base < V ? base : V - 4;  // in bounds; dropped below
+      const u32x4 q = __builtin_nontemporal_load((const u32x4*)(x + at));
+      f[s][0] = __uint_as_float(q.x);
+      f[s][1] = __uint_as_float(q.y);
+      f[s][2] = __uint_as_float(q.z);
+      f[s][3] = __uint_as_float(q.w);
+    } else {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t q = q0 + u * kArgmaxThreads;
-      if (q < nv) {
-        arg_take(b, f[u].x, 4 * q);
-        arg_take(b, f[u].y, 4 * q + 1);
-        arg_take(b, f[u].z, 4 * q + 2);
-        arg_take(b, f[u].w, 4 * q + 3);
-      }
+      for (int e = 0; e < 4; ++e) f[s][e] = x[base + e < V ? base + e : V - 1];
     }
   }
-  for (uint32_t i = 4 * nv + tid; i < V; i += kArgmaxThreads) arg_take(b, x[i], i);  // higher ids than above
-  for (int o = 32; o >= 1; o >>= 1) arg_merge(b, __shfl_xor(b.v, o), (uint32_t)__shfl_xor((int)b.i, o));
-  if ((tid & 63) == 0) {
-    s_v[tid >> 6] = b.v;
-    s_i[tid >> 6] = b.i;
-  }
+  uint64_t best = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t i = c0 + s * kThreads * 4 + tid * 4 + e;
+      const uint64_t k = i < V ? arg_key<ONE>(f[s][e], i) : 0ull;
+      best = k > best ? k : best;
+    }
+  best = wave_max_u64(best);
+  if ((tid & 63) == 0) s_best[tid >> 6] = best;
   __syncthreads();
-  if (tid == 0) {
-    ArgBest r{s_v[0], s_i[0]};
-    for (int w = 1; w < kArgmaxThreads / 64; ++w) arg_merge(r, s_v[w], s_i[w]);
-    const bool none = r.i == 0xffffffffu;
-    if (out_token) out_token[row] = none ? 0u : r.i;
-    if (out_val) out_val[row] = none ? floor_v : r.v;
+  if (tid != 0) return;
+  uint64_t b = s_best[0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) b = s_best[w] > b ? s_best[w] : b;
+  if (S == 1) {
+    arg_write<ONE>(b, row, out_token, out_val);
+    return;
   }
+  __hip_atomic_fetch_max(&g_arg_best[row], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // release: this block's maximum precedes its ticket; acquire: the last
+  // block's read follows every ticket
+  const uint32_t t = __hip_atomic_fetch_add(&g_arg_ticket[row], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  if (t + 1u != S) return;
+  const uint64_t k = __hip_atomic_exchange(&g_arg_best[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&g_arg_ticket[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  arg_write<ONE>(k, row, out_token, out_val);
+}
+
+template <bool ONE, int NS>
+static void launch_argmax_ns(bool vec, uint32_t grid, hipStream_t st, const float* x, uint32_t V, int64_t ld,
+                             uint32_t S, uint32_t* tok, float* val) {
+  if (vec)
+    hipLaunchKernelGGL((argmax_kernel<ONE, NS, true>), dim3(grid), dim3(kThreads), 0, st, x, V, ld, S, tok, val);
+  else
+    hipLaunchKernelGGL((argmax_kernel<ONE, NS, false>), dim3(grid), dim3(kThreads), 0, st, x, V, ld, S, tok, val);
+}
+
+// Rows [0, rows) of one launch (rows <= kArgRows); one: the batch-1 rule.
+static hipError_t launch_argmax(bool one, const float* x, uint32_t V, int64_t ld, uint32_t rows, uint32_t* tok,
+                                float* val, hipStream_t st) {
+  const bool vec = ((uintptr_t)x % 16u) == 0 && ld % 4 == 0 && V % 4 == 0;
+  int ns = 1;  // the largest chunk that still gives >= 1024 blocks
+  for (int c = 8; c >= 1; c >>= 1) {
+    const uint64_t S = (V + (uint64_t)c * 1024u - 1) / ((uint64_t)c * 1024u);
+    if (S * rows >= 1024u || c == 1) {
+      ns = c;
+      break;
+    }
+  }
+  const uint32_t S = (uint32_t)((V + (uint64_t)ns * 1024u - 1) / ((uint64_t)ns * 1024u));
+  const uint32_t grid = rows * S;
+  switch (ns) {
+    case 8: one ? launch_argmax_ns<true, 8>(vec, grid, st, x, V, ld, S, tok, val)
+                : launch_argmax_ns<false, 8>(vec, grid, st, x, V, ld, S, tok, val); break;
+    case 4: one ? launch_argmax_ns<true, 4>(vec, grid, st, x, V, ld, S, tok, val)
+                : launch_argmax_ns<false, 4>(vec, grid, st, x, V, ld, S, tok, val); break;
+    case 2: one ? launch_argmax_ns<true, 2>(vec, grid, st, x, V, ld, S, tok, val)
+                : launch_argmax_ns<false, 2>(vec, grid, st, x, V, ld, S, tok, val); break;
+    default: one ? launch_argmax_ns<true, 1>(vec, grid, st, x, V, ld, S, tok, val)
+                 : launch_argmax_ns<false, 1>(vec, grid, st, x, V, ld, S, tok, val); break;
+  }
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- host side
@@ -3094,10 +3193,15 @@ int oxs_argmax(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t 
                float* out_max_val, void* stream) {
   if (batch == 0) return OXS_OK;
   if (vocab == 0) return OXS_ERR_SHAPE_MISMATCH;
-  if (!logits || !out_token || logits_ld < (int64_t)vocab) return OXS_ERR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL(oxs::argmax_kernel, dim3(batch), dim3(oxs::kArgmaxThreads), 0, (hipStream_t)stream, logits,
-                     vocab, logits_ld, out_token, out_max_val);
-  return hipGetLastError() == hipSuccess ? OXS_OK : OXS_ERR_HIP;
+  if (!logits || !out_token || logits_ld < (int64_t)vocab || vocab > (1u << 30)) return OXS_ERR_INVALID_ARGUMENT;
+  for (uint32_t r0 = 0; r0 < batch; r0 += oxs::kArgRows) {  // groups of rows that share the slots in turn
+    const uint32_t rows = batch - r0 < oxs::kArgRows ? batch - r0 : oxs::kArgRows;
+    const hipError_t e = oxs::launch_argmax(batch == 1, logits + (size_t)r0 * (size_t)logits_ld, vocab, logits_ld,
+                                            rows, out_token + r0, out_max_val ? out_max_val + r0 : nullptr,
+                                            (hipStream_t)stream);
+    if (e != hipSuccess) return OXS_ERR_HIP;
+  }
+  return OXS_OK;
 }
 
 int oxs_read_floor(const float* logits, uint32_t vocab, int64_t logits_ld, uint32_t batch, uint32_t* sink,

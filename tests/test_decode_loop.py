@@ -412,38 +412,120 @@ def test_host_wait_reads_tagged_slots():
 
 # ----------------------------------------------------------------------------- the CUDA backend's argmax
 
+def _rev5(x):
+    return int(f"{x:05b}"[::-1], 2)
+
+
+def _argmax_closed_form(row, batch):
+    """launch_cuda_argmax's winner written from its reduction's structure, not
+    by simulating it: among the ids holding the largest value above -1e30, the
+    thread whose warp (then lane; with one row, block then warp then lane)
+    index has the smallest bit reversal, and that thread's first such id. A
+    left-biased strict-'>' tree over lanes l, l + 16, l + 8, ... compares bit 0
+    of the lane index last, bit 4 first (sampling_dfa.cu:26-33)."""
+    v = np.asarray(row, np.float32)
+    ok = v > np.float32(-1e30)
+    if not ok.any():
+        return 0
+    idx = np.nonzero(ok & (v == v[ok].max()))[0]
+
+    def prio(i):
+        i = int(i)
+        if batch == 1:
+            g = i % 6144
+            return (_rev5(g >> 8), _rev5((g >> 5) & 7), _rev5(g & 31), i)
+        t = i % 1024
+        return (_rev5(t >> 5), _rev5(t & 31), i)
+
+    return int(min(idx, key=prio))
+
+
 def test_oracle_argmax_floor_cases():
     # launch_cuda_argmax's floor: only values strictly above -1e30 are taken
     inf, nan = np.inf, np.nan
-    cases = [([1.0, 3.0, 3.0], (1, 3.0)), ([-inf, nan], (0, -1e30)), ([-1e30, -2e30], (0, -1e30)),
+    # [1, 3, 3]: ids 1 and 2 are lanes 1 and 2 of warp 0; the tree's offset-2
+    # step hands lane 2's 3.0 to lane 0, and lane 1's equal 3.0 never replaces
+    # it at offset 1, so id 2 wins (not the lower id)
+    cases = [([1.0, 3.0, 3.0], (2, 3.0)), ([-inf, nan], (0, -1e30)), ([-1e30, -2e30], (0, -1e30)),
              ([-1e30, -9.9e29], (1, -9.9e29)), ([nan, 2.0, inf, inf], (2, inf)), ([-5.0], (0, -5.0))]
-    for row, (tok, val) in cases:
-        got = oracle.argmax_floor_host(np.array(row, np.float32))
-        assert got[0] == tok and got[1] == np.float32(val), row
+    for batch in (1, 2):
+        for row, (tok, val) in cases:
+            got = oracle.argmax_floor_host(np.array(row, np.float32), batch)
+            assert got[0] == tok and got[1] == np.float32(val), (row, batch)
     rng = np.random.default_rng(3)
     x = rng.standard_normal(5000).astype(np.float32)
-    x[[10, 4000]] = 7.0
+    x[[10, 4000]] = 7.0  # warp 0 (reversal 0) beats warp 29 (reversal 23)
     assert oracle.argmax_floor_host(x) == (10, 7.0)
-    # -0.0 equals +0.0: the first of them wins and keeps its own sign bit
+    # -0.0 equals +0.0: the layout's winner keeps its own sign bit (id 2, lane 2)
     tok, val = oracle.argmax_floor_host(np.array([-1.0, -0.0, 0.0, -3.0], np.float32))
-    assert tok == 1 and np.float32(val).view(np.uint32) == 0x80000000
+    assert tok == 2 and np.float32(val).view(np.uint32) == 0
     tok, val = oracle.argmax_floor_host(np.array([-1.0, 0.0, -0.0], np.float32))
-    assert tok == 1 and np.float32(val).view(np.uint32) == 0
+    assert tok == 2 and np.float32(val).view(np.uint32) == 0x80000000
+
+
+def test_oracle_argmax_tie_rule_is_the_reference_layouts():
+    # ties at 42752 (thread 768 = warp 24) and 85504 (thread 512 = warp 16) of a
+    # 128256-id row: warp 16's reversal (1) beats warp 24's (3); with one row,
+    # 42752 = block 23 (reversal 29) of the 24-block layout, 85504 = block 21
+    # (reversal 21)
+    x = np.random.default_rng(7).standard_normal(128256).astype(np.float32)
+    x[[42752, 85504]] = 9.0
+    assert oracle.argmax_floor_host(x, 2) == (85504, 9.0)
+    assert oracle.argmax_floor_host(x, 1) == (85504, 9.0)
+    # lanes 8 and 16 of warp 0: reversal 2 against 1, so the higher thread wins
+    # (a lowest-thread rule would give 8)
+    y = np.full(64, -1.0, np.float32)
+    y[[8, 16]] = 2.0
+    assert oracle.argmax_floor_host(y, 2)[0] == 16
+    # one row: blocks 1 and 2 (ids 256 and 512) have reversals 16 and 8
+    z = np.full(7000, -1.0, np.float32)
+    z[[256, 512]] = 2.0
+    assert oracle.argmax_floor_host(z, 1)[0] == 512
+    assert oracle.argmax_floor_host(z, 2)[0] == 512  # (warps 8 and 16 of one block: reversals 2 and 1)
+    # one thread's ids: its first maximum (ids 5 and 1029 are both thread 5)
+    w = np.full(3000, -1.0, np.float32)
+    w[[5, 1029]] = 4.0
+    assert oracle.argmax_floor_host(w, 2)[0] == 5
+
+
+def test_oracle_argmax_against_closed_form():
+    rng = np.random.default_rng(11)
+    for trial in range(200):
+        V = int(rng.integers(1, 30000))
+        batch = int(rng.choice([1, 2]))
+        x = rng.standard_normal(V).astype(np.float32)
+        pos = rng.integers(0, V, int(rng.integers(1, 7)))
+        if trial % 3 == 0:  # ties at zero, signs mixed
+            x = -np.abs(x) - np.float32(0.5)
+            x[pos] = np.float32(0.0)
+            x[pos[::2]] = np.float32(-0.0)
+        else:
+            x[pos] = np.float32(6.0)
+        got = oracle.argmax_floor_host(x, batch)
+        assert got[0] == _argmax_closed_form(x, batch), (V, batch, pos.tolist())
+        assert np.float32(got[1]).view(np.uint32) == x[got[0]].view(np.uint32)
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,V,ld", [(1, 1, 1), (1, 128256, 128256), (5, 1001, 1003), (64, 32000, 32000),
-                                    (3, 7, 8)])
+                                    (3, 7, 8), (64, 128256, 128256), (2, 300001, 300004), (1, 7000, 7000),
+                                    (16390, 12, 12)])
 def test_gpu_argmax_matches_oracle(torch_gpu, B, V, ld):
     t = torch_gpu
     rng = np.random.default_rng(B * V)
     x = rng.standard_normal((B, ld)).astype(np.float32)
-    x[:, V // 3] = x[:, (2 * V) // 3] = np.float32(9.0)  # ties: the lower id
+    x[:, V // 3] = x[:, (2 * V) // 3] = np.float32(9.0)  # ties: the reference layout's winner
+    if V >= 85505:
+        x[0, [42752, 85504]] = np.float32(12.0)  # the two rules differ here (85504 wins)
+    if V >= 513:
+        x[-1, [256, 512]] = np.float32(15.0)  # one row: block 2 beats block 1 (512)
+    if V >= 17:
+        x[min(B - 1, 1), [8, 16]] = np.float32(20.0)  # lanes 8 and 16: 16 wins
     if B > 2:
         x[1, :] = -np.inf
         x[2, : V // 2] = np.nan
         x[2, V // 2:] = np.float32(-2e30)
-    if B > 3:  # the maximum is zero, -0.0 first: its bits come back
+    if B > 3:  # the maximum is zero, both signs: the winner's bits come back
         x[3, :] = np.float32(-1.0)
         x[3, V // 5] = np.float32(-0.0)
         x[3, V // 2] = np.float32(0.0)
@@ -452,10 +534,17 @@ def test_gpu_argmax_matches_oracle(torch_gpu, B, V, ld):
     tok = t.zeros(B, dtype=t.int32, device="cuda")
     val = t.zeros(B, dtype=t.float32, device="cuda")
     lib = _abi.load_library()
-    _abi.check(lib.oxs_argmax(ctypes.c_void_p(d.data_ptr()), V, ld, B, ctypes.c_void_p(tok.data_ptr()),
-                              ctypes.c_void_p(val.data_ptr()), None), "oxs_argmax")
-    t.cuda.synchronize()
-    got_bits = val.cpu().numpy().view(np.uint32)
-    for b in range(B):
-        want = oracle.argmax_floor_host(x[b, :V])
-        assert int(tok[b]) == want[0] and got_bits[b] == np.float32(want[1]).view(np.uint32), (b, int(tok[b]), want)
+    for call in range(2):  # the second call finds the row slots cleared by the first
+        _abi.check(lib.oxs_argmax(ctypes.c_void_p(d.data_ptr()), V, ld, B, ctypes.c_void_p(tok.data_ptr()),
+                                  ctypes.c_void_p(val.data_ptr()), None), "oxs_argmax")
+        t.cuda.synchronize()
+        got_tok = tok.cpu().numpy()
+        got_bits = val.cpu().numpy().view(np.uint32)
+        rows = range(B) if B <= 64 else list(range(8)) + list(range(B - 8, B))
+        for b in rows:
+            want = oracle.argmax_floor_host(x[b, :V], B)
+            assert int(got_tok[b]) == want[0] and got_bits[b] == np.float32(want[1]).view(np.uint32), \
+                (call, b, int(got_tok[b]), want)
+        if B > 64:  # the middle rows: all equal shape, the ties at V // 3 and 2V // 3
+            mid = np.array([oracle.argmax_floor_host(x[b, :V], B)[0] for b in range(8, B - 8, 997)])
+            assert (got_tok[8:B - 8:997] == mid).all()

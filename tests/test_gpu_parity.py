@@ -152,6 +152,10 @@ def mixed_workload(B, V, seed):
                            penalize_nl=True),
         wl.disabled_config(temperature=1.0, dry_multiplier=1.5, dry_base=1.1, dry_allowed_length=0, dry_range=300,
                            top_k=30),
+        # dry_base < 0: penalties of alternating sign (powf of a negative base, integer exponents), so DRY
+        # can raise a value and the row takes the exact re-scan
+        wl.disabled_config(temperature=0.9, dry_multiplier=0.7, dry_base=-1.3, dry_allowed_length=1, dry_range=200,
+                           top_k=60, repeat_penalty=1.05, repeat_last_n=24),
     ]
     configs = [base[i % len(base)] for i in range(B)]
     cap = 300

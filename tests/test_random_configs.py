@@ -50,7 +50,7 @@ def random_config(rng, V):
         kw["mirostat_eta"] = float(rng.choice([0.1, 0.3]))
     if rng.random() < 0.25:
         kw["dry_multiplier"] = float(rng.choice([0.5, 1.5]))
-        kw["dry_base"] = float(rng.choice([1.1, 1.75]))
+        kw["dry_base"] = float(rng.choice([1.1, 1.75, -1.2]))  # (< 0: alternating-sign penalties)
         kw["dry_allowed_length"] = int(rng.choice([0, 2, 3]))
         kw["dry_range"] = int(rng.choice([16, 128, 1024, 4096]))
     if coin():
