@@ -2522,32 +2522,31 @@ __device__ __forceinline__ uint32_t arg_index(uint32_t pr) {
   }
 }
 template <bool ONE>
-__device__ __forceinline__ uint64_t arg_key(float v, uint32_t i) {
-  const uint32_t u = __float_as_uint(v);
-  const uint64_t k = ((uint64_t)f2ord(v) << 32) | (arg_priority<ONE>(i) << 1) | (u == 0x80000000u ? 1u : 0u);
-  return v > -1e30f ? k : 0ull;  // (false for NaN)
-}
-template <bool ONE>
 __device__ __forceinline__ void arg_write(uint64_t k, uint32_t row, uint32_t* out_token, float* out_val) {
   uint32_t tok = 0;
   float val = -1e30f;
   if (k) {
     const uint32_t o = (uint32_t)(k >> 32);
     tok = arg_index<ONE>((uint32_t)k >> 1);
+    // bit 0 is the winner's sign bit: it tells -0.0 from +0.0
     val = o == 0x80000000u ? ((k & 1u) ? -0.0f : 0.0f) : ord2f(o);
   }
   out_token[row] = tok;
   if (out_val) out_val[row] = val;
 }
 
-// One block per (row, chunk of NS * 1024 logits); NS 16-byte loads per thread
-// in flight (VEC: 16-byte aligned rows, V % 4 == 0), or scalar loads.
-template <bool ONE, int NS, bool VEC>
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restrict__ logits, uint32_t V, int64_t ld,
+// One block of TH threads per (row, chunk of NS * 4 * TH logits); NS 16-byte
+// loads per thread in flight (VEC: 16-byte aligned rows, V % 4 == 0), or
+// scalar loads. Each
+// lane first takes the largest of its values (from -1e30, so that only larger
+// values count; fmaxf drops NaN), then, among its values equal to it, the
+// largest (priority << 1 | sign bit): its key. Keys reduce by maximum.
+template <bool ONE, int NS, bool VEC, int TH>
+__global__ __launch_bounds__(TH) void argmax_kernel(const float* __restrict__ logits, uint32_t V, int64_t ld,
                                                           uint32_t S, uint32_t* __restrict__ out_token,
                                                           float* __restrict__ out_val) {
-  constexpr uint32_t CH = NS * kThreads * 4;
-  __shared__ uint64_t s_best[kWavesPerBlock];
+  constexpr uint32_t CH = NS * TH * 4;
+  __shared__ uint64_t s_best[TH / 64];
   const uint32_t tid = threadIdx.x;
   const uint32_t row = blockIdx.x / S, chunk = blockIdx.x - row * S;
   const uint32_t c0 = chunk * CH;
@@ -2555,7 +2554,7 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restric
   float f[NS][4];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    const uint32_t base = c0 + s * kThreads * 4 + tid * 4;
+    const uint32_t base = c0 + s * TH * 4 + tid * 4;
     if constexpr (VEC) {
       const uint32_t at = base < V ? base : V - 4;  // in bounds; dropped below
       const u32x4 q = __builtin_nontemporal_load((const u32x4*)(x + at));
@@ -2568,68 +2567,93 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restric
       for (int e = 0; e < 4; ++e) f[s][e] = x[base + e < V ? base + e : V - 1];
     }
   }
-  uint64_t best = 0;
+  if (c0 + CH > V) {  // the row's last chunk: ids past V drop out
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c0 + s * TH * 4 + tid * 4 + e >= V) f[s][e] = neg_inf();
+  }
+  float m = -1e30f;
 #pragma unroll
   for (int s = 0; s < NS; ++s)
 #pragma unroll
+    for (int e = 0; e < 4; ++e) m = fmaxf(m, f[s][e]);
+  uint32_t lo = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t base = c0 + s * TH * 4 + tid * 4;
+#pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t i = c0 + s * kThreads * 4 + tid * 4 + e;
-      const uint64_t k = i < V ? arg_key<ONE>(f[s][e], i) : 0ull;
-      best = k > best ? k : best;
+      const uint32_t c = __builtin_amdgcn_alignbit(arg_priority<ONE>(base + e), __float_as_uint(f[s][e]), 31);
+      lo = max(lo, f[s][e] == m ? c : 0u);
     }
+  }
+  uint64_t best = m > -1e30f ? ((uint64_t)f2ord(m) << 32) | lo : 0ull;
   best = wave_max_u64(best);
   if ((tid & 63) == 0) s_best[tid >> 6] = best;
   __syncthreads();
   if (tid != 0) return;
   uint64_t b = s_best[0];
 #pragma unroll
-  for (int w = 1; w < kWavesPerBlock; ++w) b = s_best[w] > b ? s_best[w] : b;
+  for (int w = 1; w < TH / 64; ++w) b = s_best[w] > b ? s_best[w] : b;
   if (S == 1) {
     arg_write<ONE>(b, row, out_token, out_val);
     return;
   }
-  __hip_atomic_fetch_max(&g_arg_best[row], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // release: this block's maximum precedes its ticket; acquire: the last
-  // block's read follows every ticket
-  const uint32_t t = __hip_atomic_fetch_add(&g_arg_ticket[row], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  // The row's blocks meet in its slot. The ticket is issued only once this
+  // block's maximum has returned, i.e. has been performed where device-scope
+  // atomics on the slot are serialised; the row's last ticket therefore
+  // follows every block's maximum, and its exchange reads (and clears) the
+  // final one. Atomics only: no other memory is handed between blocks, so no
+  // cache write-back or invalidation is needed.
+  const uint64_t old = __hip_atomic_fetch_max(&g_arg_best[row], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t one = 1u;
+  asm volatile("" : "+v"(one) : "v"(old));  // `one` now depends on the returned maximum
+  const uint32_t t = __hip_atomic_fetch_add(&g_arg_ticket[row], one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (t + 1u != S) return;
   const uint64_t k = __hip_atomic_exchange(&g_arg_best[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(&g_arg_ticket[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   arg_write<ONE>(k, row, out_token, out_val);
 }
 
-template <bool ONE, int NS>
+template <bool ONE, int NS, int TH>
 static void launch_argmax_ns(bool vec, uint32_t grid, hipStream_t st, const float* x, uint32_t V, int64_t ld,
                              uint32_t S, uint32_t* tok, float* val) {
   if (vec)
-    hipLaunchKernelGGL((argmax_kernel<ONE, NS, true>), dim3(grid), dim3(kThreads), 0, st, x, V, ld, S, tok, val);
+    hipLaunchKernelGGL((argmax_kernel<ONE, NS, true, TH>), dim3(grid), dim3(TH), 0, st, x, V, ld, S, tok, val);
   else
-    hipLaunchKernelGGL((argmax_kernel<ONE, NS, false>), dim3(grid), dim3(kThreads), 0, st, x, V, ld, S, tok, val);
+    hipLaunchKernelGGL((argmax_kernel<ONE, NS, false, TH>), dim3(grid), dim3(TH), 0, st, x, V, ld, S, tok, val);
 }
 
 // Rows [0, rows) of one launch (rows <= kArgRows); one: the batch-1 rule.
+// Chunks of 32768, 16384, 8192 or 4096 logits (1024-thread blocks), else
+// 1024 (256 threads): the largest that still gives a block per CU. Larger
+// chunks mean fewer blocks meeting in a row's slot, whose atomics queue on
+// one address: 16 blocks per row cost 1.3 us more than 4 at 64 x 128256.
 static hipError_t launch_argmax(bool one, const float* x, uint32_t V, int64_t ld, uint32_t rows, uint32_t* tok,
                                 float* val, hipStream_t st) {
   const bool vec = ((uintptr_t)x % 16u) == 0 && ld % 4 == 0 && V % 4 == 0;
-  int ns = 1;  // the largest chunk that still gives >= 1024 blocks
-  for (int c = 8; c >= 1; c >>= 1) {
-    const uint64_t S = (V + (uint64_t)c * 1024u - 1) / ((uint64_t)c * 1024u);
-    if (S * rows >= 1024u || c == 1) {
-      ns = c;
+  constexpr uint32_t chunks[5] = {32768, 16384, 8192, 4096, 1024};
+  int pick = 4;
+  for (int c = 0; c < 4; ++c)
+    if ((V + (uint64_t)chunks[c] - 1) / chunks[c] * rows >= 256u) {
+      pick = c;
       break;
     }
-  }
-  const uint32_t S = (uint32_t)((V + (uint64_t)ns * 1024u - 1) / ((uint64_t)ns * 1024u));
+  const uint32_t S = (uint32_t)((V + (uint64_t)chunks[pick] - 1) / chunks[pick]);
   const uint32_t grid = rows * S;
-  switch (ns) {
-    case 8: one ? launch_argmax_ns<true, 8>(vec, grid, st, x, V, ld, S, tok, val)
-                : launch_argmax_ns<false, 8>(vec, grid, st, x, V, ld, S, tok, val); break;
-    case 4: one ? launch_argmax_ns<true, 4>(vec, grid, st, x, V, ld, S, tok, val)
-                : launch_argmax_ns<false, 4>(vec, grid, st, x, V, ld, S, tok, val); break;
-    case 2: one ? launch_argmax_ns<true, 2>(vec, grid, st, x, V, ld, S, tok, val)
-                : launch_argmax_ns<false, 2>(vec, grid, st, x, V, ld, S, tok, val); break;
-    default: one ? launch_argmax_ns<true, 1>(vec, grid, st, x, V, ld, S, tok, val)
-                 : launch_argmax_ns<false, 1>(vec, grid, st, x, V, ld, S, tok, val); break;
+  switch (pick) {
+    case 0: one ? launch_argmax_ns<true, 8, 1024>(vec, grid, st, x, V, ld, S, tok, val)
+                : launch_argmax_ns<false, 8, 1024>(vec, grid, st, x, V, ld, S, tok, val); break;
+    case 1: one ? launch_argmax_ns<true, 4, 1024>(vec, grid, st, x, V, ld, S, tok, val)
+                : launch_argmax_ns<false, 4, 1024>(vec, grid, st, x, V, ld, S, tok, val); break;
+    case 2: one ? launch_argmax_ns<true, 2, 1024>(vec, grid, st, x, V, ld, S, tok, val)
+                : launch_argmax_ns<false, 2, 1024>(vec, grid, st, x, V, ld, S, tok, val); break;
+    case 3: one ? launch_argmax_ns<true, 1, 1024>(vec, grid, st, x, V, ld, S, tok, val)
+                : launch_argmax_ns<false, 1, 1024>(vec, grid, st, x, V, ld, S, tok, val); break;
+    default: one ? launch_argmax_ns<true, 1, 256>(vec, grid, st, x, V, ld, S, tok, val)
+                 : launch_argmax_ns<false, 1, 256>(vec, grid, st, x, V, ld, S, tok, val); break;
   }
   return hipGetLastError();
 }
