@@ -19,7 +19,7 @@ constexpr int kUnionMax = 2048;   // candidate key slots per row
 constexpr int kUnionBig = 4096;   // ... for rows of more than 64 wavefront records (V > 16 chunks)
 constexpr int kTailArea = 4096;   // 64-bit words of tail LDS shared by the scatter, sort, exact-path table and chain scratch
 constexpr int kMaxM = 1024;       // largest max(top_k, 256) run on the device
-constexpr int kMaxChunk = 8192;   // logits per stream block
+constexpr int kMaxChunk = 8192;   // logits per stream block (at most) and per exact-path table chunk
 constexpr int kMaxChunks = 64;    // chunks per row
 constexpr int kBuckets = 256;     // tail counting-sort buckets
 constexpr int kRecPer = kMaxChunks * kWavesPerBlock / 64;  // wavefront records per lane a tail wavefront reads
@@ -999,9 +999,8 @@ __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowX
     const int shift = 56 - 8 * d;
     hist[tid] = 0;
     __syncthreads();
-    for (uint32_t c = 0; c < p.S; ++c) {
-      const uint32_t c0 = c * p.CH;
-      const uint32_t c1 = min(c0 + p.CH, p.V);
+    for (uint32_t c0 = 0; c0 < p.V; c0 += (uint32_t)kMaxChunk) {  // table chunks (the LDS table's size)
+      const uint32_t c1 = min(c0 + (uint32_t)kMaxChunk, p.V);
       if (r.any_special) build_table(p, r, row, c0, c1, table);
       for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
         const float y = transformed_logit<DT>(p, r, row, i, c0, table);
@@ -1033,9 +1032,8 @@ __device__ __forceinline__ uint32_t exact_select_row(const Params& p, const RowX
   }
   if (tid == 0) ts.counter = 0;
   __syncthreads();
-  for (uint32_t c = 0; c < p.S; ++c) {
-    const uint32_t c0 = c * p.CH;
-    const uint32_t c1 = min(c0 + p.CH, p.V);
+  for (uint32_t c0 = 0; c0 < p.V; c0 += (uint32_t)kMaxChunk) {
+    const uint32_t c1 = min(c0 + (uint32_t)kMaxChunk, p.V);
     if (r.any_special) build_table(p, r, row, c0, c1, table);
     for (uint32_t i = c0 + tid; i < c1; i += kThreads) {
       const uint32_t k = cand_key(transformed_logit<DT>(p, r, row, i, c0, table));
@@ -1684,7 +1682,7 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t k, float vmax, float scal
 // Fallback selection: all kept register keys (bit q of vm) into tmp, a bitonic
 // sort, the first meff into out. Returns the number of kept keys.
 template <int PER>
-__device__ uint32_t sort_select(const uint64_t (&lk)[PER], uint32_t vm, uint32_t M, uint64_t* tmp,
+__device__ __forceinline__ uint32_t sort_select(const uint64_t (&lk)[PER], uint32_t vm, uint32_t M, uint64_t* tmp,
                                 uint64_t* out, TailShared& ts) {
   const uint32_t cnt = (uint32_t)__popc(vm);
   uint32_t n;

@@ -15,7 +15,9 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
                                                         const uint32_t* __restrict__ wave_count,
                                                         const uint64_t* __restrict__ libm, uint32_t S, uint32_t cap_w,
                                                         uint32_t cap_shift, uint32_t rpx, uint32_t B, const Params p) {
-  __shared__ __align__(16) uint64_t s_keys[kTailArea];  // bucket scatter / sort / exact-path table / chain scratch
+  // bucket scatter / sort / exact-path table / chain scratch, and 8 words of
+  // padding for the bucket ranking's reads past a bucket
+  __shared__ __align__(16) uint64_t s_keys[kTailArea + 8];
   static_assert(kTailArea >= PER * kThreads && kTailArea * 2 >= kMaxChunk, "tail LDS area");
   __shared__ __align__(16) uint64_t s_top[kMaxM];       // sorted top-M keys (sort and exact paths)
   __shared__ __align__(16) uint32_t s_ids[kChainLd];
@@ -272,8 +274,16 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
       const uint64_t k = s_keys[i];
       const uint32_t b = bucket_of(k, vmax, scale);
       const uint32_t lo = s_bstart[b], hi = lo + s_bcount[b];
+      // eight members per step, all read before any is compared (entries past
+      // the bucket, up to 7 words into the padding, are masked out)
       uint32_t rank = lo;
-      for (uint32_t j = lo; j < hi; ++j) rank += s_keys[j] > k ? 1u : 0u;
+      for (uint32_t j = lo; j < hi; j += 8) {
+        uint64_t a[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) a[t] = s_keys[j + t];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) rank += (j + t < hi && a[t] > k) ? 1u : 0u;
+      }
       if (rank < meff) {
         s_ids[rank] = ~(uint32_t)k;
         s_pr[rank] = dexpf(key_value(k) - vmax, s_tab);
