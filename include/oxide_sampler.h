@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define OXS_ABI_VERSION 3u
+#define OXS_ABI_VERSION 4u
 
 /* Return codes. EngineError (crates/oxide-core/src/error.rs:6) has one variant
  * on this path, ShapeMismatch (error.rs:52; sampler.rs:179-181). */
@@ -53,8 +53,9 @@ extern "C" {
 #define OXS_ROW_HISTORY_FULL 2  /* Ok(token), but the device history had no room to record it */
 #define OXS_ROW_UNSUPPORTED 3   /* the row needs more than the sampler was sized for: a pool max(top_k, 256)
                                    (at most V) above oxs_limits.max_top_k, or a DRY pass penalising more
-                                   distinct ids than a row's DRY list holds (8192; 2048 through
-                                   oxs_sample_batch_static); token 0 */
+                                   distinct ids than oxs_limits.max_dry_ids (2048 through
+                                   oxs_sample_batch_static, which also refuses pools above 1024);
+                                   token 0 */
 #define OXS_ROW_MISSING_STATE 4 /* a Mirostat row but oxs_batch.mirostat_mu is NULL; token 0 */
 
 /* MirostatMode, sampler.rs:77-82. */
@@ -116,6 +117,13 @@ typedef struct oxs_limits {
   uint32_t max_vocab;  /* V per row */
   uint32_t max_top_k;  /* largest top_k any row may use; 0 means 256. Above 1024 the sampler also
                           holds [max_batch] x ~36 bytes x max_top_k of workspace for those rows */
+  uint32_t max_dry_ids; /* most distinct ids one row's DRY pass may penalise over a slice
+                           (min(history_len, dry_range), sampler.rs:394-396) longer than 1024 ids;
+                           0 means 8192 (at least 1024 is kept). The sampler holds [max_batch] x
+                           32 bytes x (max_dry_ids, kept to max_vocab, rounded up to a power of two)
+                           for these rows: 256 KiB per row at 8192. A slice of n ids penalises at most min(n, V) ids, so
+                           max_dry_ids >= min(longest slice, max_vocab) runs every DRY row; a row
+                           that penalises more returns OXS_ROW_UNSUPPORTED */
 } oxs_limits;
 
 /*
@@ -264,6 +272,10 @@ int oxs_sample_batch(oxs_sampler* sampler, const oxs_batch* batch, void* stream)
  * loops and harnesses that forbid hipMalloc.
  *   - batches up to OXS_STATIC_MAX_BATCH rows of up to OXS_STATIC_MAX_VOCAB
  *     logits; larger: OXS_ERR_LIMITS;
+ *   - sized as a sampler with max_top_k = 1024 and a DRY list of 2048 ids:
+ *     a row whose pool max(top_k, 256) (at most V) exceeds 1024, or whose DRY
+ *     pass penalises more than 2048 distinct ids, returns OXS_ROW_UNSUPPORTED
+ *     (token 0) while the other rows run;
  *   - runs on the calling thread's current device; the first call on a device
  *     sets the array up (finds its address and fills its constant tables,
  *     waiting for that on `stream`), so it must not be under stream capture

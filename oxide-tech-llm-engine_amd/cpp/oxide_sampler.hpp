@@ -232,7 +232,7 @@ class AcademicSamplerEngine {
     if (!handle_ || V > vocab_ || kept_ld > top_k_) {
       if (handle_) detail::oxs_check(oxs_sampler_destroy(handle_), "oxs_sampler_destroy");
       handle_ = nullptr;
-      oxs_limits lim{1, std::max(V, vocab_), std::max(kept_ld, top_k_)};
+      oxs_limits lim{1, std::max(V, vocab_), std::max(kept_ld, top_k_), 0u};
       int dev = 0;
       detail::hip_check(hipGetDevice(&dev), "hipGetDevice");
       detail::oxs_check(oxs_sampler_create(&handle_, &lim, dev), "oxs_sampler_create");

@@ -329,7 +329,8 @@ struct oxs_sampler {
   uint64_t* libm;
   uint64_t* dry_list;
   uint32_t* dry_count;
-  uint32_t* dry_ghash;  // [max_batch][3][2 * kDryListBig]
+  uint32_t* dry_ghash;  // [max_batch][3][2 * dry_cap]
+  uint32_t dry_cap;     // a row's DRY list entries: max_dry_ids kept to max_vocab, a power of two
   uint32_t* row_steps;  // [max_batch] decode steps each row has handed to the host
   uint32_t* path_counts;  // [kPathKinds] rows per top-M selection path
   uint64_t* wide_keys;    // rows with top_k > 1024 (max_top_k > 1024 only), else NULL
@@ -435,7 +436,7 @@ static oxs::Workspace sampler_workspace(const oxs_sampler* s) {
   w.dry_list = s->dry_list;
   w.dry_count = s->dry_count;
   w.dry_ghash = s->dry_ghash;
-  w.dry_cap = oxs::kDryListBig;
+  w.dry_cap = s->dry_cap;
   w.row_steps = s->row_steps;
   w.path_counts = s->count_paths ? s->path_counts : nullptr;
   w.wide_keys = s->wide_keys;
@@ -515,6 +516,14 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
   s->limits.max_top_k = mtk;
   const size_t B = limits->max_batch;
   const size_t W = (size_t)oxs::kMaxChunks * oxs::kWavesPerBlock;
+  {  // a slice penalises at most V distinct ids; slices of up to kDryMax ids (the LDS pass) always fit
+    const uint32_t asked = limits->max_dry_ids ? limits->max_dry_ids : (uint32_t)oxs::kDryListBig;
+    const uint32_t want = min(max(asked, (uint32_t)oxs::kDryMax), limits->max_vocab);
+    uint32_t cap = 2;
+    while (cap < want) cap <<= 1;
+    s->dry_cap = cap;
+  }
+  const size_t dcap = s->dry_cap;
   // rows over 16 chunks (more than 64 wavefront records) use the 4096-key union
   const size_t b_lists =
       B * (size_t)(limits->max_vocab > 16u * (uint32_t)oxs::kMaxChunk ? oxs::kUnionBig : oxs::kUnionMax) *
@@ -525,8 +534,8 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
                   hipMalloc((void**)&s->wave_theta, b_theta) == hipSuccess &&
                   hipMalloc((void**)&s->wave_count, b_count) == hipSuccess &&
                   hipMalloc((void**)&s->libm, oxs::kLibmWords * sizeof(uint64_t)) == hipSuccess &&
-                  hipMalloc((void**)&s->dry_list, B * oxs::kDryListBig * sizeof(uint64_t)) == hipSuccess &&
-                  hipMalloc((void**)&s->dry_ghash, B * 6 * oxs::kDryListBig * sizeof(uint32_t)) == hipSuccess &&
+                  hipMalloc((void**)&s->dry_list, B * dcap * sizeof(uint64_t)) == hipSuccess &&
+                  hipMalloc((void**)&s->dry_ghash, B * 6 * dcap * sizeof(uint32_t)) == hipSuccess &&
                   hipMalloc((void**)&s->dry_count, B * sizeof(uint32_t)) == hipSuccess &&
                   hipMalloc((void**)&s->row_steps, B * sizeof(uint32_t)) == hipSuccess &&
                   hipMemset(s->row_steps, 0, B * sizeof(uint32_t)) == hipSuccess &&
@@ -543,7 +552,7 @@ int oxs_sampler_create(oxs_sampler** out, const oxs_limits* limits, int device) 
     b_wide = b_wk + b_wa;
   }
   s->bytes = b_lists + b_theta + b_count + oxs::kLibmWords * sizeof(uint64_t) +
-             B * (oxs::kDryListBig * (sizeof(uint64_t) + 6 * sizeof(uint32_t)) + 2 * sizeof(uint32_t)) +
+             B * (dcap * (sizeof(uint64_t) + 6 * sizeof(uint32_t)) + 2 * sizeof(uint32_t)) +
              oxs::kPathKinds * sizeof(uint32_t) +
              b_wide;
   if (ok) {  // the libm tables, as bit patterns, in the workspace

@@ -26,7 +26,7 @@ constexpr int kRecPer = kMaxChunks * kWavesPerBlock / 64;  // wavefront records 
 constexpr int kDryMax = 1024;      // longest DRY history slice copied into LDS (longer ones are read in place)
 constexpr int kDryHash = 2048;     // DRY id hash slots in LDS (slices of up to kDryMax ids)
 constexpr int kDryList = kDryHash;  // entries of a row's DRY list without a global DRY hash (the static workspace)
-constexpr int kDryListBig = 8192;   // ... with one: the most distinct ids a longer slice may penalise
+constexpr int kDryListBig = 8192;   // ... with one, when oxs_limits.max_dry_ids is 0
 constexpr int kHistUnroll = 4;    // history-window ids per stream thread read with the logits
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -1754,10 +1754,10 @@ __device__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint
     cnt[h] = 0;
   }
   const uint32_t allowed = min(r.dry_allowed, 33u);
-  if (tid <= 32u && tid >= allowed)  // pen(ml), :408-409
-    ts.dry_pen[tid] = r.dry_mult * dpowf(r.dry_base, (float)(tid - allowed), tab);
   if (tid == 0) ts.counter = 0;
-  __syncthreads();
+  __syncthreads();  // (also orders the caller's libm tables in LDS before the dpowf below)
+  if (tid <= 32u && tid >= allowed)  // pen(ml), :408-409, read after the next barrier
+    ts.dry_pen[tid] = r.dry_mult * dpowf(r.dry_base, (float)(tid - allowed), tab);
   for (uint32_t q = tid; q < L; q += kThreads) {
     const uint32_t lim = min(q, 32u);
     uint32_t k = 0;
@@ -1889,18 +1889,13 @@ __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32
     dry_pass_lds<DT>(p, r, row, L, lds, tab, ts, p.dry_list + (size_t)row * p.dry_cap);
     return true;  // (at most L <= kDryHash / 2 distinct ids)
   }
-  const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
-  const bool in_lds = false;
-  const bool global = !in_lds && p.dry_ghash;
+  const uint32_t* sl = p.history + (size_t)row * p.history_ld + (r.hlen - L);  // read in place
+  const bool global = p.dry_ghash != nullptr;
   const uint32_t slots = global ? 2u * p.dry_cap : (uint32_t)kDryHash;  // a power of two
   const uint32_t shift = 32u - (31u - __builtin_clz(slots));
-  uint32_t* slice = lds;  // [kDryMax]
-  uint32_t* hkey = global ? p.dry_ghash + (size_t)row * 3 * slots : slice + kDryMax;  // ids (kEmptySlot: free)
+  uint32_t* hkey = global ? p.dry_ghash + (size_t)row * 3 * slots : lds + kDryMax;  // ids (kEmptySlot: free)
   uint32_t* cnt = hkey + slots;                // matches at the current length
   float* val = (float*)(cnt + slots);          // values
-  if (in_lds)
-    for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
-  const uint32_t* sl = in_lds ? (const uint32_t*)slice : hs;
   for (uint32_t h = tid; h < slots; h += kThreads) {
     hkey[h] = kEmptySlot;
     cnt[h] = 0;
@@ -1969,8 +1964,8 @@ __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32
     for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = ~dl[i];
     wide_sort(dl, nd, (uint64_t*)lds);
     for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = ~dl[i];
-  } else {  // (id << 32 | value bits) from the LDS table into registers, then into LDS: over the
-            // cleared counters (at most kDryMax ids: the table stays for dry_lookup), or over the start
+  } else {  // (id << 32 | value bits) from the LDS table into registers, then into LDS over the
+            // start of the area, the table included (its entries are in registers by then)
     constexpr int kPerT = kDryHash / kThreads;
     uint64_t mine[kPerT];
     uint32_t held = 0;  // bit q: slot tid + q * kThreads holds an id
@@ -1982,7 +1977,7 @@ __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32
       if (id != kEmptySlot) held |= 1u << q;
     }
     __syncthreads();
-    uint64_t* keys = in_lds ? (uint64_t*)cnt : (uint64_t*)lds;  // [kDryMax] or [kDryHash]
+    uint64_t* keys = (uint64_t*)lds;  // [kDryHash]
 #pragma unroll
     for (int q = 0; q < kPerT; ++q)
       if ((held >> q) & 1u) keys[atomicAdd(&ts.counter, 1u)] = mine[q];

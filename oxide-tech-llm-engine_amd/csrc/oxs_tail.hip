@@ -155,7 +155,9 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   for (int q = 0; q < PER; ++q) {
     const uint32_t slot = 2u * (tid + (q / 2) * kThreads) + (q & 1);
     const uint64_t k = lk[q];
-    if (slot < span && (slot & (cap_w - 1u)) < lc[q / 2] && k != 0ull) {
+    // (a key whose value word is 0, -inf or NaN: a candidate that DRY sent
+    // there, is not valid)
+    if (slot < span && (slot & (cap_w - 1u)) < lc[q / 2] && (k >> 32) != 0ull) {
       valid |= 1u << q;
       kmn = k < kmn ? k : kmn;
     }

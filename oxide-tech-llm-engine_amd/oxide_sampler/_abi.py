@@ -12,7 +12,7 @@ from pathlib import Path
 PKG_ROOT = Path(__file__).resolve().parent.parent  # oxide-tech-llm-engine_amd/
 LIB_PATH = PKG_ROOT / "lib" / "liboxide_sampler.so"
 
-OXS_ABI_VERSION = 3
+OXS_ABI_VERSION = 4
 
 OXS_OK = 0
 OXS_ERR_INVALID_ARGUMENT = -1
@@ -116,6 +116,7 @@ class OxsLimits(ctypes.Structure):
         ("max_batch", ctypes.c_uint32),
         ("max_vocab", ctypes.c_uint32),
         ("max_top_k", ctypes.c_uint32),
+        ("max_dry_ids", ctypes.c_uint32),
     ]
 
 

@@ -166,15 +166,16 @@ def _torch():
 class BatchSampler:
     """One `oxs_sampler` handle: preallocated workspace, batched launches."""
 
-    def __init__(self, max_batch: int, max_vocab: int, max_top_k: int = 256, device: int = 0):
+    def __init__(self, max_batch: int, max_vocab: int, max_top_k: int = 256, device: int = 0,
+                 max_dry_ids: int = 0):
         self.lib = load_library()
         self.torch = _torch()
         self.device = device
-        lim = OxsLimits(max_batch, max_vocab, max_top_k)
+        lim = OxsLimits(max_batch, max_vocab, max_top_k, max_dry_ids)
         h = ctypes.c_void_p()
         check(self.lib.oxs_sampler_create(ctypes.byref(h), ctypes.byref(lim), device), "oxs_sampler_create")
         self.handle = h
-        self.limits = (max_batch, max_vocab, max_top_k)
+        self.limits = (max_batch, max_vocab, max_top_k, max_dry_ids)
 
     def close(self) -> None:
         if getattr(self, "handle", None):

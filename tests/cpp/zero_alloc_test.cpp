@@ -11,8 +11,10 @@
 // separately, every call made while the window is open (the HIP runtime's
 // included, reported for information). Device: hipMemGetInfo before and after.
 //
-// The window covers 1000 oxs_sample_batch calls and 1000 oxs_decode_step calls
-// on a config-2 shaped batch (64 x 128256 f32), after a warm-up. Prints one
+// The window covers 1000 oxs_sample_batch calls, 1000 oxs_decode_step calls
+// and 1000 oxs_sample_batch_static calls on a config-2 shaped batch
+// (64 x 128256 f32), after a warm-up (for the static entry point, its set-up
+// call on the device). Prints one
 // JSON line; exits 0 when the library made no host allocation and the device's
 // free memory did not change.
 #include <hip/hip_runtime.h>
@@ -138,7 +140,7 @@ int main() {
   hipStream_t st;
   HIP_OK(hipStreamCreate(&st));
 
-  oxs_limits lim = {B, V, 256};
+  oxs_limits lim = {B, V, 256, 0};
   oxs_sampler* s = nullptr;
   OXS_OK_(oxs_sampler_create(&s, &lim, 0));
 
@@ -236,6 +238,7 @@ int main() {
     OXS_OK_(oxs_sample_batch(s, &b, st));
     OXS_OK_(oxs_decode_step(s, &bd, &io, st));
   }
+  OXS_OK_(oxs_sample_batch_static(&b, st));  // the no-allocation entry point's set-up call on this device
   HIP_OK(hipStreamSynchronize(st));
   HIP_OK(hipMemcpy(d_hlen, hlen.data(), B * 4, hipMemcpyHostToDevice));
   HIP_OK(hipDeviceSynchronize());
@@ -243,22 +246,25 @@ int main() {
   HIP_OK(hipMemGetInfo(&free0, &total));
 
   g_on.store(true);
-  int rc_sample = OXS_OK, rc_decode = OXS_OK;
+  int rc_sample = OXS_OK, rc_decode = OXS_OK, rc_static = OXS_OK;
   for (int i = 0; i < kCalls && rc_sample == OXS_OK; ++i) rc_sample = oxs_sample_batch(s, &b, st);
   for (int i = 0; i < kCalls && rc_decode == OXS_OK; ++i) rc_decode = oxs_decode_step(s, &bd, &io, st);
+  for (int i = 0; i < kCalls && rc_static == OXS_OK; ++i) rc_static = oxs_sample_batch_static(&b, st);
   g_on.store(false);
 
   HIP_OK(hipStreamSynchronize(st));
   HIP_OK(hipMemGetInfo(&free1, &total));
   const uint64_t lib_allocs = g_lib_allocs.load(), all_allocs = g_all_allocs.load();
-  printf("{\"sample_batch_calls\": %d, \"decode_step_calls\": %d, \"rc_sample\": %d, \"rc_decode\": %d, "
+  printf("{\"sample_batch_calls\": %d, \"decode_step_calls\": %d, \"sample_batch_static_calls\": %d, "
+         "\"rc_sample\": %d, \"rc_decode\": %d, \"rc_static\": %d, "
          "\"library_host_allocations\": %llu, \"process_host_allocations\": %llu, "
          "\"device_free_bytes_before\": %zu, \"device_free_bytes_after\": %zu}\n",
-         kCalls, kCalls, rc_sample, rc_decode, (unsigned long long)lib_allocs, (unsigned long long)all_allocs,
-         free0, free1);
+         kCalls, kCalls, kCalls, rc_sample, rc_decode, rc_static, (unsigned long long)lib_allocs,
+         (unsigned long long)all_allocs, free0, free1);
   fflush(stdout);
   oxs_host_free(host_tokens);
   oxs_sampler_destroy(s);
-  const bool ok = rc_sample == OXS_OK && rc_decode == OXS_OK && lib_allocs == 0 && free0 == free1;
+  const bool ok = rc_sample == OXS_OK && rc_decode == OXS_OK && rc_static == OXS_OK && lib_allocs == 0 &&
+                  free0 == free1;
   return ok ? 0 : 1;
 }

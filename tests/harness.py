@@ -52,17 +52,18 @@ def run_oracle(w: Workload, kept_ld: int = 256, record: bool = True, use_rng: bo
 _SAMPLERS = {}
 
 
-def gpu_sampler(max_batch: int, max_vocab: int, max_top_k: int = 256, exact_limits: bool = False):
+def gpu_sampler(max_batch: int, max_vocab: int, max_top_k: int = 256, exact_limits: bool = False,
+                max_dry_ids: int = 0):
     """A cached BatchSampler at least this large (exactly these limits with exact_limits)."""
     from oxide_sampler import BatchSampler
-    key = (max_batch, max_vocab, max_top_k)
+    key = (max_batch, max_vocab, max_top_k, max_dry_ids)
     if key not in _SAMPLERS:
-        for (b, v, k), s in _SAMPLERS.items():
+        for (b, v, k, d), s in _SAMPLERS.items():
             if exact_limits:
                 break
-            if b >= max_batch and v >= max_vocab and k >= max_top_k:
+            if b >= max_batch and v >= max_vocab and k >= max_top_k and d == max_dry_ids:
                 return s
-        _SAMPLERS[key] = BatchSampler(max_batch, max_vocab, max_top_k)
+        _SAMPLERS[key] = BatchSampler(max_batch, max_vocab, max_top_k, max_dry_ids=max_dry_ids)
     return _SAMPLERS[key]
 
 
@@ -78,10 +79,10 @@ def to_device(w: Workload, torch):
 def run_gpu(w: Workload, torch, kept_ld: int = 256, record: bool = True, use_rng: bool = False,
             rng_state: Optional[np.ndarray] = None, logits_out: bool = False, logits_dev=None,
             max_top_k: int = 256, shared_mask: bool = False, no_alloc: bool = False,
-            exact_limits: bool = False) -> Result:
+            exact_limits: bool = False, max_dry_ids: int = 0) -> Result:
     d = torch.device("cuda")
     cfg, bias_ids, bias_vals, ban_ids = w.packed_configs()
-    s = gpu_sampler(w.batch, w.vocab, max_top_k, exact_limits)
+    s = gpu_sampler(w.batch, w.vocab, max_top_k, exact_limits, max_dry_ids)
     logits = logits_dev if logits_dev is not None else to_device(w, torch)
     hist = torch.from_numpy(w.history.view(np.int32).copy()).to(d)
     hlen = torch.from_numpy(w.history_len.view(np.int32).copy()).to(d)

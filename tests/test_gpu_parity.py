@@ -317,25 +317,32 @@ def test_dry_long_slices(torch_gpu):
             RTOL_F32, "dry long")
 
 
-def test_dry_more_penalised_ids_than_the_list_holds(torch_gpu):
-    # history [A, B, x_i] x 9000 with distinct x_i, ending in [A, B]: the length-2 suffix matches
-    # before every x_i, so 9000 distinct ids take a DRY penalty, more than a row's 8192-entry DRY
-    # list holds: that row reports OXS_ROW_UNSUPPORTED (token 0); the other rows are unaffected
+def dry_many_ids_workload(n_ids: int, seed: int, dry_base: float = 1.75):
+    """dry_long_workload(8, 32000) whose row 3 has the history [A, B, x_i] x n_ids with distinct x_i,
+    ending in [A, B]: the length-2 suffix matches before every x_i, so n_ids distinct ids take a DRY
+    penalty."""
     V = 32000
-    w = dry_long_workload(8, V, seed=32)
+    w = dry_long_workload(8, V, seed=seed)
     a, b = 7, 11
-    xs = np.arange(100, 9100, dtype=np.uint32)
+    xs = np.arange(100, 100 + n_ids, dtype=np.uint32)
     trip = np.stack([np.full(len(xs), a, np.uint32), np.full(len(xs), b, np.uint32), xs], axis=1).reshape(-1)
     seq = np.concatenate([trip, np.array([a, b], np.uint32)])
-    hist = np.zeros((8, len(seq) + 100), np.uint32)
+    hist = np.zeros((8, max(len(seq) + 100, w.history.shape[1])), np.uint32)
     hist[:, :w.history.shape[1]] = w.history
     hist[3, :len(seq)] = seq
     w.history = hist
     w.history_len = w.history_len.copy()
     w.history_len[3] = len(seq)
-    w.configs[3] = wl.disabled_config(temperature=0.9, dry_multiplier=0.8, dry_base=1.75, dry_allowed_length=2,
+    w.configs[3] = wl.disabled_config(temperature=0.9, dry_multiplier=0.8, dry_base=dry_base, dry_allowed_length=2,
                                       dry_range=30000)
-    banner("DRY row with 9000 distinct penalised ids")
+    return w
+
+
+def test_dry_more_penalised_ids_than_the_list_holds(torch_gpu):
+    # 9000 distinct penalised ids: more than the default max_dry_ids (8192), so with the default
+    # limits that row reports OXS_ROW_UNSUPPORTED (token 0) and the other rows are unaffected
+    w = dry_many_ids_workload(9000, seed=32)
+    banner("DRY row with 9000 distinct penalised ids, default max_dry_ids")
     g = run_gpu(w, torch_gpu, kept_ld=256)
     r = run_oracle(w, kept_ld=256)
     assert g.status[3] == _abi.OXS_ROW_UNSUPPORTED and g.tokens[3] == 0
@@ -343,6 +350,18 @@ def test_dry_more_penalised_ids_than_the_list_holds(torch_gpu):
     np.testing.assert_array_equal(g.tokens[keep], r.tokens[keep])
     np.testing.assert_array_equal(g.status[keep], r.status[keep])
     np.testing.assert_array_equal(g.history_len[keep], r.history_len[keep])
+
+
+@pytest.mark.parametrize("dry_base", [1.75, -1.2])
+def test_dry_many_ids_with_max_dry_ids(torch_gpu, dry_base):
+    # the same row on a sampler created with max_dry_ids = V (every row fits): full parity, the
+    # logits write-back included; dry_base < 0 sends the row to the exact re-scan, which reads
+    # every penalised id's DRY value from the row's list
+    w = dry_many_ids_workload(9000, seed=32, dry_base=dry_base)
+    banner(f"DRY row with 9000 distinct penalised ids, max_dry_ids = V, dry_base {dry_base}")
+    g = run_gpu(w, torch_gpu, kept_ld=256, logits_out=True, max_dry_ids=w.vocab)
+    assert g.status[3] == _abi.OXS_ROW_OK
+    compare(g, run_oracle(w, kept_ld=256, logits_out=True), RTOL_F32, "dry many ids")
 
 
 def test_mixed_configs_device_rng(torch_gpu):
