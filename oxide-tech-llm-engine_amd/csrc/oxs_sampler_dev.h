@@ -824,6 +824,8 @@ struct TailShared {
   uint32_t sel_digit, sel_above, sel_count, counter;
   uint32_t dry_full;  // the DRY pass found more distinct ids than its hash holds
   float dry_pen[33];  // DRY penalty per match length (dry_pass_lds)
+  uint32_t dry_hist[kWavesPerBlock][64];  // per wavefront: occurrences per match length (dry_pass_lds)
+  uint32_t dry_bits[2];  // bit (id * 0x9e3779b1) >> 26 of every penalised id (dry_pass_lds)
   uint32_t a_kmax[kWavesPerBlock];  // per-wavefront largest keys (DRY candidate rows)
 };
 
@@ -1739,8 +1741,9 @@ static_assert(kDryOcc + kDryMax <= 2 * kTailArea, "DRY LDS layout fits the tail 
 // sorted by slot with a counting sort, and each slot's thread runs its id's
 // subtractions. Leaves the hash (ids, values) in LDS for dry_lookup.
 template <int DT>
-__device__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint32_t L, uint32_t* lds,
-                             const LibmTables& tab, TailShared& ts, uint64_t* dl) {
+__device__ __forceinline__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint32_t L,
+                                             uint32_t* lds, const LibmTables& tab, TailShared& ts, uint64_t* dl,
+                                             const uint32_t (&sv)[4], bool have_sv) {
   const uint32_t tid = threadIdx.x;
   uint32_t* slice = lds + kDrySlice;
   uint32_t* hkey = lds + kDryKey;
@@ -1748,29 +1751,78 @@ __device__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint
   uint32_t* cnt = lds + kDryCnt;
   uint32_t* occ = lds + kDryOcc;
   const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
-  for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
+  static_assert(kDryMax <= 4 * kThreads, "four slice ids per thread");
+  if (have_sv) {  // the caller read them ahead (slice_ahead)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (tid + (uint32_t)i * kThreads < L) slice[tid + (uint32_t)i * kThreads] = sv[i];
+  } else {
+    for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
+  }
   for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
     hkey[h] = kEmptySlot;
     cnt[h] = 0;
   }
   const uint32_t allowed = min(r.dry_allowed, 33u);
-  if (tid == 0) ts.counter = 0;
+  if (tid == 0) {
+    ts.counter = 0;    // occurrences
+    ts.sel_above = 0;  // penalised ids with at most 8 occurrences
+    ts.sel_count = 0;  // ... with more
+    ts.sel_digit = 0;  // distinct penalised ids
+    ts.dry_bits[0] = 0;
+    ts.dry_bits[1] = 0;
+  }
   __syncthreads();  // (also orders the caller's libm tables in LDS before the dpowf below)
   if (tid <= 32u && tid >= allowed)  // pen(ml), :408-409, read after the next barrier
     ts.dry_pen[tid] = r.dry_mult * dpowf(r.dry_base, (float)(tid - allowed), tab);
-  for (uint32_t q = tid; q < L; q += kThreads) {
+  // lambda(q) for this thread's (at most four) positions q = tid + 256 i, eight
+  // comparisons per step, all of a step's LDS reads issued before any compare.
+  // An id seen for the first time has its logit (and mask word) loaded at once
+  // and used after the loop, so those global reads overlap the rest of it.
+  const uint32_t last = L ? slice[L - 1] : 0u;  // the slice's last id
+  uint32_t first_h[4];
+  float first_x[4];
+  bool first_m[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    first_h[i] = kEmptySlot;
+    first_x[i] = 0.0f;
+    first_m[i] = true;
+    const uint32_t q = tid + (uint32_t)i * kThreads;
+    if (q >= L) continue;
     const uint32_t lim = min(q, 32u);
     uint32_t k = 0;
-    while (k < lim && slice[q - 1 - k] == slice[L - 1 - k]) ++k;  // lambda(q)
+    if (lim > 0 && slice[q - 1] == last) k = 1;  // most positions end here
+    while (k > 0 && k < lim) {
+      uint32_t a[8], b[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t kk = k + (uint32_t)t;
+        a[t] = slice[kk < lim ? q - 1 - kk : 0u];
+        b[t] = slice[kk < lim ? L - 1 - kk : 0u];
+      }
+      uint32_t run = 0;
+      bool go = true;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        go = go && k + (uint32_t)t < lim && a[t] == b[t];
+        run += go ? 1u : 0u;
+      }
+      k += run;
+      if (run < 8u) break;
+    }
     const uint32_t next = slice[q];
     if (k < allowed || next >= p.V) continue;  // no length in [allowed, k]; logits.get_mut(next) is None
     uint32_t h = (next * 0x9e3779b1u) >> 21;
     for (int probe = 0; probe < kDryHash; ++probe) {  // at most L <= kDryHash / 2 distinct ids
       const uint32_t prev = atomicCAS(&hkey[h], kEmptySlot, next);
-      if (prev == kEmptySlot) {  // first sight: the value before DRY
-        float x = load_logit<DT>(p, row, next);
-        if (p.mask && !mask_allows(p, row, next)) x = neg_inf();
-        val[h] = pre_stages_of(p, r, next, x);
+      if (prev == kEmptySlot) {  // first sight: the value before DRY, loaded now and used below
+        atomicAdd(&ts.sel_digit, 1u);
+        const uint32_t bit = (next * 0x9e3779b1u) >> 26;
+        atomicOr(&ts.dry_bits[bit >> 5], 1u << (bit & 31u));
+        first_h[i] = h;
+        first_x[i] = load_logit<DT>(p, row, next);
+        first_m[i] = !p.mask || mask_allows(p, row, next);
       }
       if (prev == kEmptySlot || prev == next) break;
       h = (h + 1) & (kDryHash - 1);
@@ -1804,49 +1856,104 @@ __device__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint
     slice[atomicAdd(&cnt[e >> 6], 1u)] = e & 63u;  // the match lengths, grouped by slot
   }
   __syncthreads();
-  // each slot's id: its subtractions, longest match length first (the slot
-  // loop kept rolled: its body is long). A slot's occurrences end at its
-  // cursor and start at the previous slot's of this thread.
-  uint32_t prev_end = start0;
-#pragma unroll 1
-  for (int j = 0; j < kPerT; ++j) {
-    const uint32_t h = tid + j * kThreads;
-    const uint32_t end = cnt[h];
-    const uint32_t n = end - prev_end;
-    prev_end = end;
-    if (n == 0) continue;
-    const uint32_t* lam = slice + cnt[h] - n;  // (the cursor ends at the range's end)
-    float v = val[h];
-    if (n <= 8u) {  // the usual case: the match lengths in registers, read once
-      uint32_t lr[8];
+  // the values before DRY of the ids this thread saw first (their loads were
+  // issued in the lambda loop)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) lr[i] = (uint32_t)i < n ? lam[i] : 0u;
-      uint32_t top = 0;
+  for (int i = 0; i < 4; ++i)
+    if (first_h[i] != kEmptySlot) {
+      const uint32_t id = hkey[first_h[i]];
+      val[first_h[i]] = pre_stages_of(p, r, id, first_m[i] ? first_x[i] : neg_inf());
+    }
+  // the penalised ids as lists of (slot << 11 | occurrences) over the free
+  // occurrence area, ids of at most 8 occurrences from its start, the others
+  // from its end (all of them there when there are at most four ids); each
+  // slot's start in cnt (a slot's occurrences end at its cursor and start at
+  // the previous slot's of this thread)
+  const bool few = ts.sel_digit <= (uint32_t)kWavesPerBlock;
+  {
+    uint32_t prev_end = start0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) top = max(top, lr[i]);
-      float pen = top >= allowed ? ts.dry_pen[top] : 0.0f;
-      for (uint32_t ml = top + 1; ml-- > allowed;) {
-        uint32_t act = 0;  // occurrences matching at this length
-#pragma unroll
-        for (int i = 0; i < 8; ++i) act += ((uint32_t)i < n && lr[i] >= ml) ? 1u : 0u;
-        const float pen_next = ml > allowed ? ts.dry_pen[ml - 1] : 0.0f;  // (read ahead)
-        uint32_t a = act;  // act subtractions of pen, four per loop step (:411)
-        for (; a >= 4u; a -= 4u) v = (((v - pen) - pen) - pen) - pen;
-        const float v2 = (v - pen) - pen;
-        v = (a & 2u) ? v2 : v;
-        const float v1 = v - pen;
-        v = (a & 1u) ? v1 : v;
-        pen = pen_next;
-      }
-    } else {  // an id with many matches: its lengths re-read per length
-      for (uint32_t ml = 33; ml-- > allowed;) {
-        uint32_t act = 0;
-        for (uint32_t i = 0; i < n; ++i) act += lam[i] >= ml ? 1u : 0u;
-        const float pen = ts.dry_pen[ml];
-        for (uint32_t a = 0; a < act; ++a) v = v - pen;  // :411
+    for (int j = 0; j < kPerT; ++j) {
+      const uint32_t h = tid + j * kThreads;
+      const uint32_t end = cnt[h];
+      const uint32_t n = end - prev_end;
+      prev_end = end;
+      if (n) {
+        const uint32_t at = n <= 8u && !few ? atomicAdd(&ts.sel_above, 1u)
+                                            : (uint32_t)kDryMax - 1u - atomicAdd(&ts.sel_count, 1u);
+        occ[at] = (h << 11) | n;  // h < 2048, n <= kDryMax
+        cnt[h] = end - n;
       }
     }
+  }
+  __syncthreads();
+  // Each id's subtractions, longest match length first (:405-413): pen(ml)
+  // once per occurrence with lambda >= ml, for ml = 32 down to allowed, each a
+  // rounded subtraction. The penalties sit in registers and the lengths are
+  // unrolled, so the only serial work is the subtractions themselves.
+  float pens[33];
+#pragma unroll
+  for (int ml = 0; ml < 33; ++ml) pens[ml] = ts.dry_pen[ml];  // (entries below allowed are never used)
+  const uint32_t n_light = ts.sel_above, n_heavy = ts.sel_count;
+  // ids of up to 8 occurrences, one per thread, their lengths as bytes of two
+  // registers (0 past n). For a length ml >= 1 each byte of
+  // 0x80808080 + (ml - 1) * 0x01010101 - P is 0x80 + ml - 1 - lambda (no
+  // borrow: lambda <= 32), whose top bit is clear exactly when lambda >= ml, so
+  // one subtraction and a bit count give the occurrences matching at ml.
+#pragma unroll 1
+  for (uint32_t c = tid; c < n_light; c += kThreads) {
+    const uint32_t h = occ[c] >> 11, n = occ[c] & 2047u;
+    const uint32_t* lam = slice + cnt[h];
+    uint32_t P0 = 0, P1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      P0 |= ((uint32_t)i < n ? lam[i] : 0u) << (8 * i);
+      P1 |= ((uint32_t)i + 4u < n ? lam[i + 4] : 0u) << (8 * i);
+    }
+    float v = val[h];
+#pragma unroll
+    for (int ml = 32; ml >= 0; --ml) {
+      const uint32_t K = 0x80808080u + (uint32_t)(ml > 0 ? ml - 1 : 0) * 0x01010101u;
+      uint32_t act = ml > 0 ? (uint32_t)(__builtin_popcount(~(K - P0) & 0x80808080u) +
+                                         __builtin_popcount(~(K - P1) & 0x80808080u))
+                            : n;  // every occurrence matches at length 0
+      act = (uint32_t)ml >= allowed ? act : 0u;
+      const float pen = pens[ml];
+      for (; act >= 2u; act -= 2u) v = (v - pen) - pen;  // act subtractions of pen (:411)
+      if (act) v = v - pen;
+    }
     val[h] = v;
+  }
+  // ids of more occurrences (or every id when there are at most four), one per
+  // wavefront: a histogram of the match lengths in LDS, then lane l holds the
+  // occurrences matching at length l (a suffix sum) and the penalty pen(l), and
+  // the subtractions run with wavefront-uniform counts read from those lanes
+  const uint32_t lane = tid & 63u, wave = tid >> 6;
+  uint32_t* hist = ts.dry_hist[wave];
+  const float pen_l = lane <= 32u && lane >= allowed ? ts.dry_pen[lane] : 0.0f;
+#pragma unroll 1
+  for (uint32_t c = wave; c < n_heavy; c += kWavesPerBlock) {
+    const uint32_t e = occ[(uint32_t)kDryMax - 1u - c];
+    const uint32_t h = e >> 11, n = e & 2047u;
+    const uint32_t* lam = slice + cnt[h];
+    hist[lane] = 0;
+    wave_sync();
+    for (uint32_t b0 = lane; b0 < n; b0 += 64) atomicAdd(&hist[lam[b0]], 1u);
+    wave_sync();
+    const uint32_t x = hist[lane];  // (lanes above 32 hold 0)
+    const uint32_t incl = wave_incl_scan(x);
+    const uint32_t act_l = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63) - incl + x;  // lambda >= lane
+    float v = val[h];
+#pragma unroll 1
+    for (int ml = 32; ml >= (int)allowed; --ml) {
+      const uint32_t na = (uint32_t)__builtin_amdgcn_readlane((int)act_l, ml);
+      const float pen = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pen_l), ml));
+      uint32_t a = 0;
+      for (; a + 4u <= na; a += 4u) v = (((v - pen) - pen) - pen) - pen;  // :411
+      for (; a < na; ++a) v = v - pen;
+    }
+    if (lane == 0) val[h] = v;
+    wave_sync();
   }
   __syncthreads();
   // the list: (id << 32 | value bits), sorted by id, built over the cursors
@@ -1863,6 +1970,21 @@ __device__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint
   for (uint32_t i = tid; i < nd; i += kThreads) dl[i] = keys[i];
   if (tid == 0) p.dry_count[row] = nd;
   __syncthreads();
+}
+
+// The DRY slice of a row whose slice fits the LDS pass (min(history_len,
+// dry_range) <= kDryMax ids), read ahead into registers: id tid + 256 i in
+// sv[i]. Returns whether it read them.
+__device__ __forceinline__ bool slice_ahead(const Params& p, const RowXf& r, uint32_t row, uint32_t (&sv)[4]) {
+  const uint32_t L = min(r.hlen, r.dry_range);
+  if (!r.dry || L == 0 || L > (uint32_t)kDryMax) return false;
+  const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t j = threadIdx.x + (uint32_t)i * kThreads;
+    sv[i] = hs[j < L ? j : 0u];
+  }
+  return true;
 }
 
 // DRY (sampler.rs:393-415) for one row, by its tail block. Over the last
@@ -1882,11 +2004,12 @@ __device__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint
 // up to kDryMax ids, the LDS hash (ids and values) is left for dry_lookup.
 template <int DT>
 __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32_t row, uint32_t* lds,
-                                         const LibmTables& tab, TailShared& ts) {
+                                         const LibmTables& tab, TailShared& ts, const uint32_t (&sv)[4],
+                                         bool have_sv) {
   const uint32_t tid = threadIdx.x;
   const uint32_t L = min(r.hlen, r.dry_range);  // :394-396
   if (L <= (uint32_t)kDryMax) {
-    dry_pass_lds<DT>(p, r, row, L, lds, tab, ts, p.dry_list + (size_t)row * p.dry_cap);
+    dry_pass_lds<DT>(p, r, row, L, lds, tab, ts, p.dry_list + (size_t)row * p.dry_cap, sv, have_sv);
     return true;  // (at most L <= kDryHash / 2 distinct ids)
   }
   const uint32_t* sl = p.history + (size_t)row * p.history_ld + (r.hlen - L);  // read in place
