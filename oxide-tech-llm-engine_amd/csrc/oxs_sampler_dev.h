@@ -1742,8 +1742,7 @@ static_assert(kDryOcc + kDryMax <= 2 * kTailArea, "DRY LDS layout fits the tail 
 // subtractions. Leaves the hash (ids, values) in LDS for dry_lookup.
 template <int DT>
 __device__ __forceinline__ void dry_pass_lds(const Params& p, const RowXf& r, uint32_t row, uint32_t L,
-                                             uint32_t* lds, const LibmTables& tab, TailShared& ts, uint64_t* dl,
-                                             const uint32_t (&sv)[4], bool have_sv) {
+                                             uint32_t* lds, const LibmTables& tab, TailShared& ts, uint64_t* dl) {
   const uint32_t tid = threadIdx.x;
   uint32_t* slice = lds + kDrySlice;
   uint32_t* hkey = lds + kDryKey;
@@ -1751,14 +1750,8 @@ __device__ __forceinline__ void dry_pass_lds(const Params& p, const RowXf& r, ui
   uint32_t* cnt = lds + kDryCnt;
   uint32_t* occ = lds + kDryOcc;
   const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
-  static_assert(kDryMax <= 4 * kThreads, "four slice ids per thread");
-  if (have_sv) {  // the caller read them ahead (slice_ahead)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (tid + (uint32_t)i * kThreads < L) slice[tid + (uint32_t)i * kThreads] = sv[i];
-  } else {
-    for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
-  }
+  static_assert(kDryMax <= 4 * kThreads, "four slice positions per thread");
+  for (uint32_t i = tid; i < L; i += kThreads) slice[i] = hs[i];
   for (uint32_t h = tid; h < (uint32_t)kDryHash; h += kThreads) {
     hkey[h] = kEmptySlot;
     cnt[h] = 0;
@@ -1889,38 +1882,36 @@ __device__ __forceinline__ void dry_pass_lds(const Params& p, const RowXf& r, ui
   __syncthreads();
   // Each id's subtractions, longest match length first (:405-413): pen(ml)
   // once per occurrence with lambda >= ml, for ml = 32 down to allowed, each a
-  // rounded subtraction. The penalties sit in registers and the lengths are
-  // unrolled, so the only serial work is the subtractions themselves.
-  float pens[33];
-#pragma unroll
-  for (int ml = 0; ml < 33; ++ml) pens[ml] = ts.dry_pen[ml];  // (entries below allowed are never used)
+  // rounded subtraction. (Kept as rolled loops: unrolling them over the 33
+  // lengths raised the whole tail kernel's register spills and slowed rows
+  // without DRY.)
   const uint32_t n_light = ts.sel_above, n_heavy = ts.sel_count;
-  // ids of up to 8 occurrences, one per thread, their lengths as bytes of two
-  // registers (0 past n). For a length ml >= 1 each byte of
-  // 0x80808080 + (ml - 1) * 0x01010101 - P is 0x80 + ml - 1 - lambda (no
-  // borrow: lambda <= 32), whose top bit is clear exactly when lambda >= ml, so
-  // one subtraction and a bit count give the occurrences matching at ml.
+  // ids of up to 8 occurrences, one per thread, their lengths in registers and
+  // the next length's penalty read ahead
 #pragma unroll 1
   for (uint32_t c = tid; c < n_light; c += kThreads) {
     const uint32_t h = occ[c] >> 11, n = occ[c] & 2047u;
     const uint32_t* lam = slice + cnt[h];
-    uint32_t P0 = 0, P1 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      P0 |= ((uint32_t)i < n ? lam[i] : 0u) << (8 * i);
-      P1 |= ((uint32_t)i + 4u < n ? lam[i + 4] : 0u) << (8 * i);
-    }
     float v = val[h];
+    uint32_t lr[8];
 #pragma unroll
-    for (int ml = 32; ml >= 0; --ml) {
-      const uint32_t K = 0x80808080u + (uint32_t)(ml > 0 ? ml - 1 : 0) * 0x01010101u;
-      uint32_t act = ml > 0 ? (uint32_t)(__builtin_popcount(~(K - P0) & 0x80808080u) +
-                                         __builtin_popcount(~(K - P1) & 0x80808080u))
-                            : n;  // every occurrence matches at length 0
-      act = (uint32_t)ml >= allowed ? act : 0u;
-      const float pen = pens[ml];
-      for (; act >= 2u; act -= 2u) v = (v - pen) - pen;  // act subtractions of pen (:411)
-      if (act) v = v - pen;
+    for (int i = 0; i < 8; ++i) lr[i] = (uint32_t)i < n ? lam[i] : 0u;
+    uint32_t top = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) top = max(top, lr[i]);
+    float pen = top >= allowed ? ts.dry_pen[top] : 0.0f;
+    for (uint32_t ml = top + 1; ml-- > allowed;) {
+      uint32_t act = 0;  // occurrences matching at this length
+#pragma unroll
+      for (int i = 0; i < 8; ++i) act += ((uint32_t)i < n && lr[i] >= ml) ? 1u : 0u;
+      const float pen_next = ml > allowed ? ts.dry_pen[ml - 1] : 0.0f;  // (read ahead)
+      uint32_t a = act;  // act subtractions of pen, four per loop step (:411)
+      for (; a >= 4u; a -= 4u) v = (((v - pen) - pen) - pen) - pen;
+      const float v2 = (v - pen) - pen;
+      v = (a & 2u) ? v2 : v;
+      const float v1 = v - pen;
+      v = (a & 1u) ? v1 : v;
+      pen = pen_next;
     }
     val[h] = v;
   }
@@ -1972,21 +1963,6 @@ __device__ __forceinline__ void dry_pass_lds(const Params& p, const RowXf& r, ui
   __syncthreads();
 }
 
-// The DRY slice of a row whose slice fits the LDS pass (min(history_len,
-// dry_range) <= kDryMax ids), read ahead into registers: id tid + 256 i in
-// sv[i]. Returns whether it read them.
-__device__ __forceinline__ bool slice_ahead(const Params& p, const RowXf& r, uint32_t row, uint32_t (&sv)[4]) {
-  const uint32_t L = min(r.hlen, r.dry_range);
-  if (!r.dry || L == 0 || L > (uint32_t)kDryMax) return false;
-  const uint32_t* hs = p.history + (size_t)row * p.history_ld + (r.hlen - L);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t j = threadIdx.x + (uint32_t)i * kThreads;
-    sv[i] = hs[j < L ? j : 0u];
-  }
-  return true;
-}
-
 // DRY (sampler.rs:393-415) for one row, by its tail block. Over the last
 // dry_range history ids, for match lengths 32 down to allowed_length, every
 // earlier position whose n-gram equals the slice's suffix penalises the id
@@ -2004,12 +1980,11 @@ __device__ __forceinline__ bool slice_ahead(const Params& p, const RowXf& r, uin
 // up to kDryMax ids, the LDS hash (ids and values) is left for dry_lookup.
 template <int DT>
 __device__ __forceinline__ bool dry_pass(const Params& p, const RowXf& r, uint32_t row, uint32_t* lds,
-                                         const LibmTables& tab, TailShared& ts, const uint32_t (&sv)[4],
-                                         bool have_sv) {
+                                         const LibmTables& tab, TailShared& ts) {
   const uint32_t tid = threadIdx.x;
   const uint32_t L = min(r.hlen, r.dry_range);  // :394-396
   if (L <= (uint32_t)kDryMax) {
-    dry_pass_lds<DT>(p, r, row, L, lds, tab, ts, p.dry_list + (size_t)row * p.dry_cap, sv, have_sv);
+    dry_pass_lds<DT>(p, r, row, L, lds, tab, ts, p.dry_list + (size_t)row * p.dry_cap);
     return true;  // (at most L <= kDryHash / 2 distinct ids)
   }
   const uint32_t* sl = p.history + (size_t)row * p.history_ld + (r.hlen - L);  // read in place

@@ -66,20 +66,6 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   const RowIn rin = load_row_in(p, row);
   const oxs_sampling_config c = rin.cfg;
   const RowXf r = make_row_xf_h(p, c, rin.history_len);
-  // a DRY row's slice and repeat-window ids, read now for its DRY pass and
-  // candidate step below (the window's first 4 x 256 ids; a longer window reads
-  // the rest there)
-  uint32_t sv[4];
-  const bool have_sv = slice_ahead(p, r, row, sv);
-  uint32_t wv[4];
-  if (r.dry && r.use_hist) {
-    const uint32_t* win = p.history + (size_t)row * p.history_ld + r.wstart;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t j = tid + (uint32_t)q * kThreads;
-      wv[q] = win[j < r.wn ? j : 0u];
-    }
-  }
   RowState rs;
   rs.uniform = rin.uniform;
   rs.mu = rin.mu;
@@ -113,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
   }
   // DRY rows: their values, then the exact path (the stream kernel's
   // candidates do not include DRY)
-  if (r.dry && !dry_pass<DT>(p, r, row, (uint32_t*)s_keys, s_tab, ts, sv, have_sv)) {
+  if (r.dry && !dry_pass<DT>(p, r, row, (uint32_t*)s_keys, s_tab, ts)) {
     count_path(p, kPathNone);
     write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);  // more penalised ids than the DRY hash holds
     return;
@@ -137,14 +123,8 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const uint64_t* __restri
     const uint64_t bits = ((uint64_t)ts.dry_bits[1] << 32) | ts.dry_bits[0];
     const auto maybe_dry = [bits](uint32_t id) { return ((bits >> ((id * 0x9e3779b1u) >> 26)) & 1u) != 0u; };
     if (r.use_hist) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (tid + (uint32_t)q * kThreads >= r.wn || !maybe_dry(wv[q])) continue;
-        const uint32_t h = dry_lookup(hkey, wv[q]);
-        if (h < (uint32_t)kDryHash) atomicAdd(&wcnt[h], 1u);
-      }
       const uint32_t* win = p.history + (size_t)row * p.history_ld + r.wstart;
-      for (uint32_t j = tid + 4u * kThreads; j < r.wn; j += kThreads) {
+      for (uint32_t j = tid; j < r.wn; j += kThreads) {
         if (!maybe_dry(win[j])) continue;
         const uint32_t h = dry_lookup(hkey, win[j]);
         if (h < (uint32_t)kDryHash) atomicAdd(&wcnt[h], 1u);
@@ -398,9 +378,7 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const Params p) {
     write_row_result<DT>(p, row, 0u, OXS_ROW_MISSING_STATE, rs);
     return;
   }
-  uint32_t sv[4];
-  const bool have_sv = slice_ahead(p, r, row, sv);
-  if (r.dry && !dry_pass<DT>(p, r, row, (uint32_t*)s_area, s_tab, ts, sv, have_sv)) {
+  if (r.dry && !dry_pass<DT>(p, r, row, (uint32_t*)s_area, s_tab, ts)) {
     count_path(p, kPathNone);
     write_row_result<DT>(p, row, 0u, OXS_ROW_UNSUPPORTED, rs);
     return;
