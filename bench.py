@@ -480,6 +480,58 @@ def bench_lm_head(args, torch):
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 
 
+def bench_argmax(args, torch):
+    """oxs_argmax, the greedy path (launch_cuda_argmax, sampling_dfa.cu:2-178), per batch shape: graph replays
+    over a pool of distinct logits batches larger than the 256 MiB MALL, so every launch reads from HBM; HIP
+    events on the launch stream; tokens checked against torch.argmax on rows without a tied maximum."""
+    from oxide_sampler import _abi  # noqa: PLC0415
+    d = torch.device("cuda")
+    lib = _abi.load_library()
+    lines = {}
+    for B, V in ((1, 128256), (8, 128256), (64, 128256), (256, 151936)):
+        n_pool = max(2, int(600e6 // (B * V * 4)) + 1)
+        g = torch.Generator(device=d)
+        g.manual_seed(0x5EED0300 + B)
+        pool = torch.randn(n_pool, B, V, device=d, generator=g)
+        tok = torch.zeros(B, dtype=torch.int32, device=d)
+        val = torch.zeros(B, dtype=torch.float32, device=d)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        n = 3 * n_pool
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(n):
+                _abi.check(lib.oxs_argmax(ctypes.c_void_p(pool[i % n_pool].data_ptr()), V, V, B,
+                                          ctypes.c_void_p(tok.data_ptr()), ctypes.c_void_p(val.data_ptr()),
+                                          ctypes.c_void_p(side.cuda_stream)), "oxs_argmax")
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        with torch.cuda.stream(side):
+            e0.record(side)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(side)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+        last = pool[(n - 1) % n_pool]
+        single = (last == last.max(dim=1, keepdim=True).values).sum(dim=1) == 1  # rows without a tied maximum
+        ok = bool(((tok.long() == torch.argmax(last, dim=1)) | ~single).all())
+        gbs = B * V * 4 / (us * 1e-6) / 1e9
+        lines[f"B{B}xV{V}"] = {"batch": B, "vocab": V, "us_per_launch": us, "GBps": gbs,
+                               "frac_of_hbm_peak": gbs / HBM_PEAK_GBS, "tokens_match_torch_argmax": ok,
+                               "pool_batches": n_pool}
+        print(f"[argmax] B={B} V={V}: {us:.2f} us per launch, {gbs:.0f} GB/s, tokens ok {ok}",
+              file=sys.stderr, flush=True)
+        assert ok, "oxs_argmax differs from torch.argmax on a tie-free batch"
+        del pool
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": "oxs_argmax (greedy decode path) per batch shape", "unit": "us/launch",
+                      "higher_is_better": False, "n_gpus": 1, "dtype": "f32",
+                      "data": "synthetic N(0,1) logits, pools larger than 600 MB", "shapes": lines}), flush=True)
+
+
 def bench_read_floor(args, torch):
     """The read floor of the stream phase on config 2: oxs_read_floor (the
     stream kernel's grid and 16-byte non-temporal loads over the same
@@ -788,7 +840,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only 8 plain 256 MiB device copies (scale for the rocprofv3 byte counters)")
     ap.add_argument("--traffic-summary", default=str(ROOT / "profiles" / "config2_pmc_traffic.json"))
-    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head", "configs", "read_floor"),
+    ap.add_argument("--workload", choices=("sample", "decode", "dfa_mask", "lm_head", "configs", "read_floor", "argmax"),
                     default="sample",
                     help="sample: the headline config-2 line; decode / dfa_mask / lm_head / configs: secondary lines")
     ap.add_argument("--config-ids", default="1,2,3,4,5,2dry",
@@ -837,6 +889,8 @@ def main():
         return
     if args.workload == "read_floor":
         return bench_read_floor(args, torch)
+    if args.workload == "argmax":
+        return bench_argmax(args, torch)
     if args.workload == "configs":
         bench_configs(args, torch)
         return
